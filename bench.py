@@ -1,0 +1,258 @@
+#!/usr/bin/env python3
+"""Benchmark of the submanifold sparse conv3d path on one MI355X.
+
+Headline (the JSON line's `value`): the neighbor-map build on ~1.5M voxels of a 1-voxel shell in
+a 512^3 grid, shuffled rows ("map512").  One step = one tsc_map_build over the whole coordinate
+set, inputs already resident in HBM.  value = algorithmic bytes (128 B/voxel: 16 B coords in,
+4 B sorted key + 108 B neighbor row out) / time, in GB/s.
+
+`secondary` carries the conv workloads measured in the same run (ms per conv, effective
+TFLOP/s counting only valid taps, algorithmic GB/s, roofline fraction):
+  conv64_f32       conv 64->64 fp32, ~25k voxels (64^3, 2-voxel shell)
+  narrow512_f16    conv 32->32 and 32->64 fp16 on the map512 voxels
+  wide128_bf16     conv 512->512 bf16, 4 x ~61k voxels (128^3 shells)
+  resblock64_bf16  4 x ResBlock (conv-LN-SiLU-conv-+x) at C=1024 bf16, 2 x ~32k voxels
+
+`roofline` is for the map build's dominant kernel, timed with hipEvents around each launch on
+the stream the library launches on; `cpu_baseline` times the PyTorch-CPU restatement of the
+reference's hashmap_fallback (torch.sort + torch.searchsorted) on the same coordinates.
+
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline] [--no-secondary]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "ms/conv + effective TFLOP/s (or GB/s) for 3^3 sparse conv at N active voxels"
+PEAK_HBM = 8.0e12          # B/s, MI355X HBM3E
+PEAK_MFMA = {"bfloat16": 2.5e15, "float16": 2.5e15, "float32": 157.3e12}  # dense FLOP/s
+MAP_BYTES_PER_VOXEL = 128  # 16 coords + 4 key + 108 table
+# Algorithmic bytes per voxel of each map-build kernel (inputs it must read + outputs it writes).
+MAP_KERNEL_BYTES = {"map_mark": 16, "map_place": 16 + 4 + 4, "map_fill": 4 + 4 + 108}
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def time_steps(fn, steps: int, warmup: int) -> float:
+    """Mean ms per step over `steps` after `warmup`, bracketed by syncs and events."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps
+
+
+def kernel_times(ctx, fn, steps: int) -> dict:
+    """{kernel: (avg ms per launch, launches per step)} from library hipEvents."""
+    import torch
+
+    torch.cuda.synchronize()
+    ctx.profile_reset()
+    ctx.profile(True)
+    for _ in range(steps):
+        fn()
+    ctx.profile(False)
+    res = ctx.profile_results()
+    ctx.profile_reset()
+    return {k: (ms / n, n / steps) for k, (ms, n) in res.items()}
+
+
+def load_traffic() -> dict:
+    p = ROOT / "profiles" / "traffic.json"
+    if p.exists():
+        try:
+            return json.loads(p.read_text())
+        except ValueError:
+            return {}
+    return {}
+
+
+def cpu_baseline(coords_np, shape, threads: int) -> dict:
+    import torch
+
+    from oracle import torch_path
+
+    torch.set_num_threads(threads)
+    c = torch.from_numpy(coords_np)
+    n = c.shape[0]
+    torch_path.hashmap_fallback(c[:1000], shape)  # warm-up
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        torch_path.hashmap_fallback(c, shape)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    return {"value": round(MAP_BYTES_PER_VOXEL * n / t / 1e9, 4), "unit": "GB/s", "cores": threads,
+            "kind": "port", "ms": round(t * 1e3, 2),
+            "sample": f"full map512 coordinate set (N={n}), torch.sort + 27 torch.searchsorted, "
+                      f"median of 3 after a warm-up, torch {torch.__version__}"}
+
+
+def conv_record(name, ms, n, p, ci, co, dtype, extra=None) -> dict:
+    s = 4 if dtype == "float32" else 2
+    flops = 2.0 * p * ci * co
+    nbytes = n * ci * s + n * co * s + 27 * ci * co * s + co * s + 108 * n
+    t = ms / 1e3
+    ideal = max(flops / PEAK_MFMA[dtype], nbytes / PEAK_HBM)
+    bound = "mfma" if flops / PEAK_MFMA[dtype] >= nbytes / PEAK_HBM else "hbm"
+    rec = {"workload": name, "dtype": dtype, "voxels": n, "valid_pairs": p, "ci": ci, "co": co,
+           "ms_per_conv": round(ms, 4), "voxels_per_s": round(n / t, 1),
+           "tflops_effective": round(flops / t / 1e12, 2), "gbps_algorithmic": round(nbytes / t / 1e9, 1),
+           "bound": bound, "roofline_frac": round(ideal / t, 4),
+           "mfma_frac": round(flops / t / PEAK_MFMA[dtype], 4)}
+    if extra:
+        rec.update(extra)
+    return rec
+
+
+def secondary(pkg, dev, steps, warmup, map512_coords) -> list:
+    import numpy as np
+    import torch
+
+    wl = pkg.workloads
+    out = []
+    dts = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16}
+    for name in ("conv64_f32", "narrow512_f16", "wide128_bf16", "resblock64_bf16"):
+        w = wl.WORKLOADS[name]
+        coords = map512_coords if w.shell == "map512" else wl.make_coords(name)
+        shape = wl.grid_shape(name)
+        batch = int(coords[:, 0].max()) + 1
+        c_dev = torch.from_numpy(coords).to(dev)
+        nmap = pkg.build_neighbor_map(c_dev, shape, batch)
+        n = coords.shape[0]
+        p = int((nmap.nbr >= 0).sum().item())
+        dt = dts[w.dtype]
+        for ci, co in w.channels:
+            f = torch.from_numpy(wl.features(n, ci, 1)).to(dev).to(dt)
+            if name == "resblock64_bf16":
+                ws = [(torch.from_numpy(wl.conv_weight(co, ci, 10 + i)).to(dev).to(dt),
+                       torch.from_numpy(wl.conv_weight(co, ci, 20 + i)).to(dev).to(dt)) for i in range(4)]
+                zero = torch.zeros(co, device=dev, dtype=dt)
+                bufs = [torch.empty_like(f) for _ in range(2)]
+
+                def chain():
+                    h = f
+                    for i, (w1, w2) in enumerate(ws):
+                        h = pkg.sparse_resblock(h, nmap, w1, zero, w2, zero, eps=1e-6, out=bufs[i % 2])
+                    return h
+                ms = time_steps(chain, max(3, steps // 4), 2)
+                rec = conv_record(name, ms / 8, n, p, ci, co, w.dtype,
+                                  {"ms_per_chain": round(ms, 3), "chain": "4 x (conv-LN-SiLU-conv-+x)",
+                                   "note": "ms_per_conv = chain time / 8 (LN+SiLU time included)"})
+                kt = kernel_times(pkg._lib.context(dev.index), chain, 2)
+            else:
+                wt = torch.from_numpy(wl.conv_weight(co, ci, 2)).to(dev).to(dt)
+                b = torch.zeros(co, device=dev, dtype=dt)
+                o = torch.empty((n, co), device=dev, dtype=dt)
+
+                def conv():
+                    return pkg.sparse_conv3d(f, wt, b, nmap, out=o)
+                ms = time_steps(conv, steps, warmup)
+                rec = conv_record(name, ms, n, p, ci, co, w.dtype)
+                kt = kernel_times(pkg._lib.context(dev.index), conv, 3)
+            rec["kernels"] = {k: {"avg_ms": round(a, 4), "launches_per_step": c} for k, (a, c) in kt.items()}
+            out.append(rec)
+            log(f"{name} {ci}->{co} {w.dtype}: {rec['ms_per_conv']} ms/conv, "
+                f"{rec['tflops_effective']} TFLOP/s eff, {rec['gbps_algorithmic']} GB/s, "
+                f"roofline {rec['roofline_frac']}")
+        del nmap, c_dev
+        torch.cuda.empty_cache()
+    return out
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: this build's sparse-conv path runs on a single "
+              "MI355X (multi-GPU sharding is design-only); run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    import __graft_entry__
+
+    pkg = __graft_entry__.load_package()
+    dev = torch.device("cuda:0")
+    wl = pkg.workloads
+    t0 = time.time()
+    coords = wl.make_coords("map512")
+    shape = wl.grid_shape("map512")
+    n = coords.shape[0]
+    log(f"map512: N={n} voxels generated in {time.time() - t0:.1f}s")
+    c_dev = torch.from_numpy(coords).to(dev)
+    nmap = pkg.build_neighbor_map(c_dev, shape, 1)  # validated once (duplicates / range)
+    torch.cuda.synchronize()
+
+    def step():
+        return pkg.build_neighbor_map(c_dev, shape, 1, validate=False)
+
+    ms = time_steps(step, args.steps, args.warmup)
+    log(f"map build: {ms:.4f} ms/step, {MAP_BYTES_PER_VOXEL * n / ms / 1e6:.1f} GB/s algorithmic")
+    ctx = pkg._lib.context(dev.index)
+    kt = kernel_times(ctx, step, args.steps)
+    dom = max(kt, key=lambda k: kt[k][0] * kt[k][1])
+    dom_ms = kt[dom][0]
+    per_voxel = MAP_KERNEL_BYTES.get(dom)
+    achieved = (per_voxel * n / (dom_ms / 1e3)) if per_voxel else None
+    traffic = load_traffic().get(f"map512/{dom}")
+    roofline = {"kernel": dom, "bound": "hbm",
+                "achieved": round(achieved / 1e9, 1) if achieved else None, "peak": PEAK_HBM / 1e9,
+                "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4) if achieved else None,
+                "traffic": traffic, "avg_ms": round(dom_ms, 4),
+                "alg_bytes_per_launch": per_voxel * n if per_voxel else None,
+                "kernels": {k: {"avg_ms": round(a, 4), "launches_per_step": c} for k, (a, c) in kt.items()}}
+    log(f"dominant kernel {dom}: {dom_ms:.4f} ms; all: " +
+        ", ".join(f"{k}={a:.4f}" for k, (a, c) in kt.items()))
+    del nmap
+    sec = []
+    if not args.no_secondary:
+        sec = secondary(pkg, dev, args.steps, args.warmup, coords)
+    cpu = None
+    if not args.no_cpu_baseline:
+        log(f"cpu baseline on {args.cpu_threads} threads ...")
+        cpu = cpu_baseline(coords, shape, args.cpu_threads)
+        log(f"cpu baseline: {cpu['ms']} ms ({cpu['value']} GB/s)")
+    line = {
+        "metric": METRIC, "value": round(MAP_BYTES_PER_VOXEL * n / (ms / 1e3) / 1e9, 2), "unit": "GB/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int32",
+        "data": "synthetic",
+        "config": {"workload": f"map512: neighbor-map build, {n} voxels, 1-voxel shell of a perturbed "
+                               f"ellipsoid in 512^3, shuffled rows, 3x3x3 dilation 1",
+                   "voxels": n, "grid": list(shape), "batch": 1,
+                   "bytes_per_voxel_algorithmic": MAP_BYTES_PER_VOXEL},
+        "roofline": roofline, "cpu_baseline": cpu, "secondary": sec,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

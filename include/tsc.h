@@ -1,0 +1,154 @@
+/*
+ * tsc.h — C ABI of libtrellis_sparse.so: TRELLIS.2 submanifold sparse conv3d on MI355X (gfx950).
+ *
+ * Every entry point takes plain pointers and sizes.  Device buffers are raw HIP device addresses
+ * (a TS host passes them as u64 / Deno "pointer"; a Python host passes tensor.data_ptr()).
+ * Every call returns an int status (TSC_OK == 0); on failure tsc_last_error() holds a message
+ * for the calling thread.  All compute calls are enqueue-only on the context's stream and
+ * return before the GPU finishes; tsc_sync() waits.
+ *
+ * Interfaces replaced (reference = johnandersen777/TRELLIS.2-stableprojectorz):
+ *   SparseConv3d.forward pass0+pass1 (neighbor map)   src/sparse/ops/conv3d.ts:62-152,
+ *        WGSL src/sparse/ops/conv3d_wgsl.ts:44-128;  Python hashmap_fallback (README.md:111)
+ *   SparseConv3d.forward pass2 (gather-GEMM-bias)     src/sparse/ops/conv3d.ts:154-221,
+ *        WGSL src/sparse/ops/conv3d_wgsl.ts:132-231;  Python conv_none (README.md:109)
+ *   layerNorm                                         src/dense/ops/layer_norm.ts:12-125
+ *   silu                                              src/dense/ops/silu.ts:11-56
+ *   add (residual)                                    src/dense/ops/elementwise.ts:22-65
+ */
+#ifndef TSC_H
+#define TSC_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TSC_VERSION 1
+
+/* Status codes returned by every entry point. */
+enum tsc_status {
+  TSC_OK = 0,
+  TSC_ERR_INVALID = 1,     /* bad argument: null pointer, bad size, misaligned buffer */
+  TSC_ERR_UNSUPPORTED = 2, /* valid request this build does not implement (e.g. kernel 5x5x5) */
+  TSC_ERR_HIP = 3,         /* a HIP runtime call failed */
+  TSC_ERR_OOM = 4          /* workspace allocation failed */
+};
+
+/* Element types of features / weights / outputs.  Accumulation is always fp32. */
+enum tsc_dtype { TSC_F32 = 0, TSC_F16 = 1, TSC_BF16 = 2 };
+
+/* Bits the map build ORs into its device status word (0 = map valid). */
+#define TSC_MAP_DUPLICATE 1u    /* two rows share one (b,x,y,z) */
+#define TSC_MAP_OUT_OF_RANGE 2u /* a coordinate outside [0,B)x[0,X)x[0,Y)x[0,Z) */
+
+/* Neighbor-map construction strategies. */
+enum tsc_map_method {
+  TSC_MAP_AUTO = 0,   /* occupancy bitmap when the grid is dense enough, else radix sort */
+  TSC_MAP_BITMAP = 1, /* occupancy bitmap + popcount rank (a one-pass counting sort) */
+  TSC_MAP_RADIX = 2   /* LSD radix sort of packed keys + binary search */
+};
+
+/* Epilogues of tsc_conv_fused. */
+enum tsc_epilogue {
+  TSC_EPI_BIAS = 0,          /* out = conv + bias */
+  TSC_EPI_BIAS_RESIDUAL = 1, /* out = conv + bias + residual            (elementwise.ts:22-47) */
+  TSC_EPI_BIAS_LN_SILU = 2   /* out = silu(layernorm(conv + bias))      (layer_norm.ts:34-65,
+                                                                         silu.ts:25-29) */
+};
+
+typedef struct tsc_ctx tsc_ctx;
+
+/* ---- library / context ------------------------------------------------------------------- */
+int tsc_version(void);
+/* Message of the last failed call on this thread ("" if none).  Valid until the next call. */
+const char* tsc_last_error(void);
+/* Context bound to one device, enqueueing on `stream` (NULL = the HIP null stream, which is also
+ * torch's default stream).  The caller owns the stream.  Not re-entrant: one host thread drives a
+ * context at a time. */
+int tsc_ctx_create(int device, void* stream, tsc_ctx** out);
+int tsc_ctx_destroy(tsc_ctx* ctx);
+/* Re-point the context at another stream (e.g. torch.cuda.current_stream()). */
+int tsc_ctx_set_stream(tsc_ctx* ctx, void* stream);
+void* tsc_ctx_stream(tsc_ctx* ctx);
+int tsc_sync(tsc_ctx* ctx);
+
+/* Device memory for hosts without an allocator (the TS host).  Caller frees with tsc_free. */
+int tsc_malloc(tsc_ctx* ctx, size_t bytes, void** out);
+int tsc_free(tsc_ctx* ctx, void* ptr);
+int tsc_memcpy_h2d(tsc_ctx* ctx, void* dst, const void* src, size_t bytes); /* synchronous */
+int tsc_memcpy_d2h(tsc_ctx* ctx, void* dst, const void* src, size_t bytes); /* synchronous */
+int tsc_memset_zero(tsc_ctx* ctx, void* dst, size_t bytes);               /* stream-ordered */
+
+/* ---- neighbor map ------------------------------------------------------------------------- */
+/* Bytes per packed key: 4 if B*X*Y*Z <= 2^31, else 8.  Keys are key = ((b*X+x)*Y+y)*Z+z. */
+int tsc_map_key_bytes(int32_t B, int32_t X, int32_t Y, int32_t Z);
+
+/* Build the submanifold neighbor map of a coordinate set.
+ *   coords      device int32 (N,4) rows [b,x,y,z], 16-byte aligned
+ *   kernel      {Kd,Kh,Kw}; only {3,3,3} is supported.  dilation {dD,dH,dW} >= 1.
+ *   nbr_out     device int32 (N,27): nbr[n*27+v] = original row of the voxel at
+ *               (x+(kd-1)dD, y+(kh-1)dH, z+(kw-1)dW), v = kd*9+kh*3+kw, or -1 when that voxel is
+ *               absent or outside [0,X)x[0,Y)x[0,Z).  Row n, tap 13 is n itself.
+ *   keys_out    optional device buffer of N keys (tsc_map_key_bytes each): sorted unique keys.
+ *   perm_out    optional device int32 (N): perm[i] = original row of the i-th sorted key.
+ *   status_dev  device uint32 (1): set to 0, then OR-ed with TSC_MAP_* bits.  Outputs are valid
+ *               only when it reads 0.
+ * Mirrors conv3d.ts:62-152 (pass0/pass1) and hashmap_fallback (README.md:111) with the batch index
+ * in the key (the WGSL grid omits it, conv3d_wgsl.ts:67). */
+int tsc_map_build(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t B, int32_t X, int32_t Y,
+                  int32_t Z, const int32_t kernel[3], const int32_t dilation[3], int32_t method,
+                  void* keys_out, int32_t* perm_out, int32_t* nbr_out, uint32_t* status_dev);
+
+/* ---- convolution -------------------------------------------------------------------------- */
+/* out[n,co] = bias[co] + sum_{v: nbr[n,v]>=0} sum_ci feats[nbr[n,v],ci] * W[co,v,ci]
+ *   feats (N,Ci), weight (Co,3,3,3,Ci), bias (Co) or NULL, out (N,Co): all `dtype`, row-major.
+ *   order: optional device int32 (N) permutation; rows are processed in that order (pass the
+ *   map's perm_out for spatial locality).  NULL = 0..N-1.  Results do not depend on it.
+ * Replaces conv3d.ts:154-221 / conv3d_wgsl.ts:132-231.  Ci and Co must be multiples of 16. */
+int tsc_conv(tsc_ctx* ctx, int32_t dtype, const void* feats, const void* weight, const void* bias,
+             const int32_t* nbr, const int32_t* order, int64_t N, int32_t Ci, int32_t Co, void* out);
+
+/* tsc_conv followed by an epilogue.  residual (N,Co) is read for TSC_EPI_BIAS_RESIDUAL;
+ * ln_gamma / ln_beta (Co, dtype, NULL = 1 / 0) and eps for TSC_EPI_BIAS_LN_SILU.
+ * out may alias residual. */
+int tsc_conv_fused(tsc_ctx* ctx, int32_t dtype, const void* feats, const void* weight,
+                   const void* bias, const int32_t* nbr, const int32_t* order, int64_t N,
+                   int32_t Ci, int32_t Co, int32_t epilogue, const void* residual,
+                   const void* ln_gamma, const void* ln_beta, float eps, void* out);
+
+/* ---- row ops (the ResBlock's epilogue semantics) ------------------------------------------ */
+/* y = (x-mean)/sqrt(var+eps)*gamma+beta per row of C, fp32 math; optional SiLU after it.
+ * gamma/beta NULL = 1/0.  y may alias x (in place, as layer_norm.ts:12-125). */
+int tsc_layernorm(tsc_ctx* ctx, int32_t dtype, const void* x, int64_t N, int32_t C,
+                  const void* gamma, const void* beta, float eps, int32_t apply_silu, void* y);
+/* y = x * sigmoid(x) elementwise, fp32 math (silu.ts:25-29).  y may alias x. */
+int tsc_silu(tsc_ctx* ctx, int32_t dtype, const void* x, int64_t numel, void* y);
+/* y = a + b elementwise, fp32 math (elementwise.ts:33-40).  y may alias a. */
+int tsc_add(tsc_ctx* ctx, int32_t dtype, const void* a, const void* b, int64_t numel, void* y);
+
+/* Sparse ResBlock: out = x + conv2(silu(LN(conv1(x)+b1))) + b2, with C=Ci=Co.
+ * LN uses eps and gamma/beta (NULL = 1/0).  out must not alias x.  The intermediate (N,C)
+ * activation lives in the context's workspace. */
+int tsc_resblock(tsc_ctx* ctx, int32_t dtype, const void* x, const int32_t* nbr,
+                 const int32_t* order, int64_t N, int32_t C, const void* w1, const void* b1,
+                 const void* ln_gamma, const void* ln_beta, float eps, const void* w2,
+                 const void* b2, void* out);
+
+/* ---- per-kernel timing -------------------------------------------------------------------- */
+/* While enabled, every kernel the context launches is bracketed by hipEvents on its stream.
+ * tsc_profile_collect syncs the stream and folds the pending launches into per-kernel totals
+ * (count of distinct kernel names in *count); tsc_profile_entry reads one total. */
+int tsc_profile_enable(tsc_ctx* ctx, int on);
+int tsc_profile_collect(tsc_ctx* ctx, int* count);
+int tsc_profile_entry(tsc_ctx* ctx, int index, char* name, int name_len, double* total_ms,
+                      int64_t* launches);
+int tsc_profile_reset(tsc_ctx* ctx);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TSC_H */

@@ -1,0 +1,155 @@
+"""CPU oracle for the submanifold sparse conv3d path — TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this package,
+and only as the checker or the timed CPU baseline; the product library never calls it.
+
+Contents
+  oracle.c          plain-C restatement (map build two ways, fp64 conv, LayerNorm, SiLU);
+                    built into liboracle.so by build() with gcc -O2 -fopenmp
+  torch_path.py     PyTorch-CPU restatement of the reference's Python path
+                    (hashmap_fallback: torch.sort + torch.searchsorted; conv_none: per-tap
+                    index_select + mm), used as the timed CPU baseline
+  brute.py          pure-Python brute force for tiny inputs
+
+Pinning (see tests/test_oracle.py): the map builds are checked against each other and against
+brute force, sorted keys against numpy.unique, the conv against a dense torch F.conv3d closed
+form in fp64, LayerNorm/SiLU against torch.nn.functional in fp64, and all of them against the
+fixtures in tests/golden/ that were generated without this package.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB = HERE / "liboracle.so"
+STATUS_DUPLICATE = 1
+STATUS_OUT_OF_RANGE = 2
+
+_lib = None
+
+
+def build(force: bool = True) -> Path:
+    """Compile oracle.c into liboracle.so (gcc, OpenMP)."""
+    src = HERE / "oracle.c"
+    if not force and LIB.exists() and LIB.stat().st_mtime >= src.stat().st_mtime:
+        return LIB
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = ["gcc", "-O2", "-fopenmp", "-shared", "-fPIC", "-o", str(tmp), str(src), "-lm"]
+    subprocess.run(cmd, check=True)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def _load():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB.exists():
+        build()
+    lib = ctypes.CDLL(str(LIB))
+    P = ctypes.c_void_p
+    i64, i32, u32, f64 = ctypes.c_int64, ctypes.c_int32, ctypes.c_uint32, ctypes.c_double
+    lib.oracle_pack_key.restype = i64
+    lib.oracle_pack_key.argtypes = [i32] * 7
+    lib.oracle_map_sorted.restype = u32
+    lib.oracle_map_sorted.argtypes = [P, i64, i32, i32, i32, i32, P, P, P, P]
+    lib.oracle_map_grid.restype = u32
+    lib.oracle_map_grid.argtypes = [P, i64, i32, i32, i32, i32, P, P]
+    lib.oracle_conv.restype = None
+    lib.oracle_conv.argtypes = [P, P, P, P, i64, i32, i32, P]
+    lib.oracle_layernorm.restype = None
+    lib.oracle_layernorm.argtypes = [P, i64, i32, P, P, f64, i32, P]
+    lib.oracle_silu.restype = None
+    lib.oracle_silu.argtypes = [P, i64, P]
+    _lib = lib
+    return lib
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _coords(coords):
+    c = np.ascontiguousarray(coords, dtype=np.int32)
+    assert c.ndim == 2 and c.shape[1] == 4
+    return c
+
+
+def pack_keys(coords, shape) -> np.ndarray:
+    """key = ((b*X+x)*Y+y)*Z+z as int64 (the packing both sides use)."""
+    c = _coords(coords).astype(np.int64)
+    X, Y, Z = shape
+    return ((c[:, 0] * X + c[:, 1]) * Y + c[:, 2]) * Z + c[:, 3]
+
+
+def map_sorted(coords, batch, shape, dilation=(1, 1, 1)):
+    """hashmap_fallback restatement.  Returns (status, sorted_keys int64, perm int32, nbr (N,27))."""
+    lib = _load()
+    c = _coords(coords)
+    n = c.shape[0]
+    keys = np.empty(n, np.int64)
+    perm = np.empty(n, np.int32)
+    nbr = np.empty((n, 27), np.int32)
+    dil = np.asarray(dilation, np.int32)
+    st = lib.oracle_map_sorted(_ptr(c), n, batch, *shape, _ptr(dil), _ptr(keys), _ptr(perm), _ptr(nbr))
+    return int(st), keys, perm, nbr
+
+
+def map_grid(coords, batch, shape, dilation=(1, 1, 1)):
+    """Dense-grid (WGSL pass0/pass1) restatement.  Returns (status, nbr (N,27))."""
+    lib = _load()
+    c = _coords(coords)
+    n = c.shape[0]
+    nbr = np.empty((n, 27), np.int32)
+    dil = np.asarray(dilation, np.int32)
+    st = lib.oracle_map_grid(_ptr(c), n, batch, *shape, _ptr(dil), _ptr(nbr))
+    return int(st), nbr
+
+
+def conv(feats, weight, bias, nbr) -> np.ndarray:
+    """fp64 gather-GEMM-bias.  weight (Co,3,3,3,Ci) or (Co,27,Ci); bias (Co,) or None."""
+    lib = _load()
+    f = np.ascontiguousarray(feats, dtype=np.float64)
+    w = np.ascontiguousarray(weight, dtype=np.float64)
+    co = w.shape[0]
+    ci = w.shape[-1]
+    w = w.reshape(co, 27, ci)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float64)
+    nb = np.ascontiguousarray(nbr, dtype=np.int32)
+    n = nb.shape[0]
+    assert f.shape == (f.shape[0], ci) and nb.shape == (n, 27)
+    assert n == 0 or (nb.max() < f.shape[0])
+    out = np.empty((n, co), np.float64)
+    lib.oracle_conv(_ptr(f), _ptr(w), _ptr(b), _ptr(nb), n, ci, co, _ptr(out))
+    return out
+
+
+def layernorm(x, gamma=None, beta=None, eps=1e-6, silu=False) -> np.ndarray:
+    lib = _load()
+    a = np.ascontiguousarray(x, dtype=np.float64)
+    n, c = a.shape
+    g = None if gamma is None else np.ascontiguousarray(gamma, dtype=np.float64)
+    b = None if beta is None else np.ascontiguousarray(beta, dtype=np.float64)
+    y = np.empty_like(a)
+    lib.oracle_layernorm(_ptr(a), n, c, _ptr(g), _ptr(b), float(eps), int(bool(silu)), _ptr(y))
+    return y
+
+
+def silu(x) -> np.ndarray:
+    lib = _load()
+    a = np.ascontiguousarray(x, dtype=np.float64)
+    y = np.empty_like(a)
+    lib.oracle_silu(_ptr(a), a.size, _ptr(y))
+    return y
+
+
+def resblock(x, nbr, w1, b1, w2, b2, gamma=None, beta=None, eps=1e-6) -> np.ndarray:
+    """x + conv2(silu(LN(conv1(x)+b1)))+b2 in fp64 (config-5 block, stated literally)."""
+    h = conv(x, w1, b1, nbr)
+    h = layernorm(h, gamma, beta, eps, silu=True)
+    return np.asarray(x, np.float64) + conv(h, w2, b2, nbr)

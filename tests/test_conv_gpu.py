@@ -1,0 +1,166 @@
+"""Sparse conv on the GPU vs the fp64 oracle.
+
+Tolerance (norm-wise relative, max|y - r| / max|r|, r computed in fp64 from the same rounded
+inputs and weights): fp32 <= 1e-4, fp16 / bf16 <= 2e-2.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests import _golden
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: 1e-4, torch.float16: 2e-2, torch.bfloat16: 2e-2}
+
+
+def rel_err(got, ref):
+    got = np.asarray(got, np.float64)
+    return float(np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+def _rounded(a, dtype, dev):
+    t = torch.from_numpy(np.ascontiguousarray(a)).to(dev).to(dtype)
+    return t, t.float().cpu().numpy().astype(np.float64)
+
+
+def _map(pkg, dev, coords, batch, shape, dil=(1, 1, 1)):
+    return pkg.build_neighbor_map(torch.from_numpy(coords).to(dev), shape, batch, dil)
+
+
+@pytest.mark.parametrize("case", ["shell_b2", "random_dil213"])
+def test_conv_golden_fp32(pkg, dev, case):
+    md, a = _golden.load(case)
+    coords = a[("in", "coords")]
+    m = _map(pkg, dev, coords, int(md["metadata"]["batch"]), _golden.meta_tuple(md, "spatial_shape"),
+             _golden.meta_tuple(md, "dilation"))
+    f = torch.from_numpy(a[("in", "feats")]).to(dev)
+    w = torch.from_numpy(a[("in", "weight")]).to(dev)
+    b = a.get(("in", "bias"))
+    b = None if b is None else torch.from_numpy(b).to(dev)
+    print(f"  conv golden {case} N={len(coords)} Ci={f.shape[1]} Co={w.shape[0]}", flush=True)
+    out = pkg.sparse_conv3d(f, w, b, m)
+    err = rel_err(out.cpu().numpy(), a[("exp", "conv_out")])
+    assert err <= 1e-4, err
+
+
+def _workload_conv(pkg, dev, workload, ci, co, dtype, sample_rows=None, seed=0, bias=True):
+    coords = pkg.workloads.make_coords(workload)
+    batch = int(coords[:, 0].max()) + 1
+    shape = pkg.workloads.grid_shape(workload)
+    n = len(coords)
+    print(f"  conv {workload} N={n} {ci}->{co} {dtype}", flush=True)
+    m = _map(pkg, dev, coords, batch, shape)
+    f, f64 = _rounded(pkg.workloads.features(n, ci, seed), dtype, dev)
+    w, w64 = _rounded(pkg.workloads.conv_weight(co, ci, seed + 1), dtype, dev)
+    bnp = np.random.default_rng(seed + 2).standard_normal(co).astype(np.float32) * 0.1
+    b, b64 = _rounded(bnp, dtype, dev) if bias else (None, None)
+    out = pkg.sparse_conv3d(f, w, b, m).float().cpu().numpy()
+    nbr = m.nbr.cpu().numpy()
+    rows = np.arange(n)
+    if sample_rows is not None and sample_rows < n:
+        rows = np.sort(np.random.default_rng(seed + 3).choice(n, sample_rows, replace=False))
+    ref = oracle.conv(f64, w64, b64, nbr[rows])
+    return rel_err(out[rows], ref), m, (f, w, b), out
+
+
+def test_conv_fp32_64_full(pkg, dev):
+    err, *_ = _workload_conv(pkg, dev, "conv64_f32", 64, 64, torch.float32)
+    assert err <= TOL[torch.float32], err
+
+
+@pytest.mark.parametrize("ci,co", [(32, 32), (32, 64)])
+def test_conv_fp16_narrow_full_size(pkg, dev, ci, co):
+    err, *_ = _workload_conv(pkg, dev, "narrow512_f16", ci, co, torch.float16, sample_rows=20000)
+    assert err <= TOL[torch.float16], err
+
+
+def test_conv_bf16_wide_full_size(pkg, dev):
+    err, *_ = _workload_conv(pkg, dev, "wide128_bf16", 512, 512, torch.bfloat16, sample_rows=600)
+    assert err <= TOL[torch.bfloat16], err
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("ci,co", [(16, 32), (64, 128), (96, 96), (128, 256), (256, 64)])
+def test_conv_dtypes_and_shapes(pkg, dev, dtype, ci, co):
+    if dtype == torch.float32 or ci * 2 % 32 == 0:
+        err, *_ = _workload_conv(pkg, dev, "resblock64_bf16", ci, co, dtype, sample_rows=800)
+        assert err <= TOL[dtype], err
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_conv_order_invariance_bit_exact(pkg, dev, dtype):
+    coords = pkg.workloads.make_coords("conv64_f32")
+    n = len(coords)
+    m = _map(pkg, dev, coords, 1, (64, 64, 64))
+    f = torch.from_numpy(pkg.workloads.features(n, 64, 5)).to(dev).to(dtype)
+    w = torch.from_numpy(pkg.workloads.conv_weight(128, 64, 6)).to(dev).to(dtype)
+    ident = pkg.sparse_conv3d(f, w, None, m.nbr)
+    sorted_ = pkg.sparse_conv3d(f, w, None, m)
+    rnd = torch.from_numpy(np.random.default_rng(1).permutation(n).astype(np.int32)).to(dev)
+    shuffled = pkg.sparse_conv3d(f, w, None, m.nbr, order=rnd)
+    assert torch.equal(ident, sorted_) and torch.equal(ident, shuffled)
+
+
+def test_conv_properties(pkg, dev):
+    """Exact identities: one-hot weights give a gather; scaling by 2 commutes; zero W = bias."""
+    coords = pkg.workloads.make_coords("conv64_f32")
+    n = len(coords)
+    m = _map(pkg, dev, coords, 1, (64, 64, 64))
+    nbr = m.nbr.cpu().numpy()
+    f = torch.from_numpy(pkg.workloads.features(n, 32, 9)).to(dev).to(torch.bfloat16)
+    for v in (0, 13, 26):
+        w = torch.zeros((32, 27, 32))
+        w[:, v, :] = torch.eye(32)
+        out = pkg.sparse_conv3d(f, w.reshape(32, 3, 3, 3, 32).to(dev).to(torch.bfloat16), None, m)
+        idx = torch.from_numpy(np.maximum(nbr[:, v], 0)).to(dev).long()
+        want = torch.where(torch.from_numpy(nbr[:, v:v + 1] >= 0).to(dev), f[idx], torch.zeros_like(f[idx]))
+        assert torch.equal(out, want), v
+    w = torch.from_numpy(pkg.workloads.conv_weight(64, 32, 3)).to(dev).to(torch.bfloat16)
+    a = pkg.sparse_conv3d(f, w, None, m)
+    b2 = pkg.sparse_conv3d(f * 2, w, None, m)
+    assert torch.equal(a.float() * 2, b2.float())
+    bias = torch.randn(64, device=dev).to(torch.bfloat16)
+    z = pkg.sparse_conv3d(f, torch.zeros_like(w), bias, m)
+    assert torch.equal(z, bias.expand(n, 64))
+
+
+def test_conv_epilogues(pkg, dev):
+    coords = pkg.workloads.make_coords("resblock64_bf16")[:4000]
+    coords = coords[coords[:, 0] == 0]
+    n = len(coords)
+    m = _map(pkg, dev, coords, 1, (64, 64, 64))
+    nbr = m.nbr.cpu().numpy()
+    dt = torch.bfloat16
+    f, f64 = _rounded(pkg.workloads.features(n, 256, 1), dt, dev)
+    w, w64 = _rounded(pkg.workloads.conv_weight(256, 256, 2), dt, dev)
+    b, b64 = _rounded(np.linspace(-1, 1, 256).astype(np.float32), dt, dev)
+    r, r64 = _rounded(pkg.workloads.features(n, 256, 3), dt, dev)
+    g, g64 = _rounded(np.linspace(0.5, 1.5, 256).astype(np.float32), dt, dev)
+    be, be64 = _rounded(np.linspace(-0.2, 0.3, 256).astype(np.float32), dt, dev)
+    base = oracle.conv(f64, w64, b64, nbr)
+    out = pkg.sparse_conv3d(f, w, b, m, epilogue="residual", residual=r)
+    assert rel_err(out.float().cpu().numpy(), base + r64) <= 2e-2
+    out = pkg.sparse_conv3d(f, w, b, m, epilogue="ln_silu", ln_weight=g, ln_bias=be, eps=1e-6)
+    ref = oracle.layernorm(base, g64, be64, 1e-6, silu=True)
+    assert rel_err(out.float().cpu().numpy(), ref) <= 2e-2
+    # in place: out aliases the residual
+    r2 = r.clone()
+    pkg.sparse_conv3d(f, w, b, m, epilogue="residual", residual=r2, out=r2)
+    assert rel_err(r2.float().cpu().numpy(), base + r64) <= 2e-2
+
+
+def test_conv_rejects_unsupported(pkg, dev):
+    coords = np.array([[0, 1, 1, 1]], np.int32)
+    m = _map(pkg, dev, coords, 1, (3, 3, 3))
+    f = torch.zeros((1, 8), device=dev, dtype=torch.float16)
+    w = torch.zeros((32, 3, 3, 3, 8), device=dev, dtype=torch.float16)
+    with pytest.raises(pkg.TscError, match="multiple of 32"):
+        pkg.sparse_conv3d(f, w, None, m)  # 8 fp16 channels = 16 bytes
+    f = torch.zeros((1, 32), device=dev, dtype=torch.float16)
+    w = torch.zeros((48, 3, 3, 3, 32), device=dev, dtype=torch.float16)
+    with pytest.raises(pkg.TscError, match="Co=48"):
+        pkg.sparse_conv3d(f, w, None, m)
+    with pytest.raises(pkg.TscError):
+        pkg.sparse_conv3d(f.cpu(), w[:32].cpu(), None, m)

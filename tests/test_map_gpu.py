@@ -1,0 +1,113 @@
+"""Neighbor-map build on the GPU vs the oracle / golden fixtures: bit-exact."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests import _golden
+
+pytestmark = pytest.mark.gpu
+
+METHODS = ["bitmap"]
+
+
+def _build(pkg, dev, coords, batch, shape, dil=(1, 1, 1), method="auto"):
+    print(f"  map_build N={len(coords)} B={batch} shape={shape} dil={dil} method={method}", flush=True)
+    c = torch.from_numpy(np.ascontiguousarray(coords, np.int32)).to(dev)
+    m = pkg.build_neighbor_map(c, shape, batch, dil, method=method)
+    torch.cuda.synchronize()
+    return m
+
+
+def _check(m, coords, batch, shape, dil):
+    st, keys, perm, nbr = oracle.map_sorted(coords, batch, shape, dil)
+    assert st == 0
+    np.testing.assert_array_equal(m.nbr.cpu().numpy(), nbr)
+    np.testing.assert_array_equal(m.keys.cpu().numpy().astype(np.int64), keys)
+    np.testing.assert_array_equal(m.perm.cpu().numpy(), perm)
+
+
+@pytest.mark.parametrize("method", METHODS)
+@pytest.mark.parametrize("case", ["shell_b2", "random_dil213"])
+def test_map_golden(pkg, dev, case, method):
+    md, a = _golden.load(case)
+    coords = a[("in", "coords")]
+    batch = int(md["metadata"]["batch"])
+    shape = _golden.meta_tuple(md, "spatial_shape")
+    dil = _golden.meta_tuple(md, "dilation")
+    m = _build(pkg, dev, coords, batch, shape, dil, method)
+    np.testing.assert_array_equal(m.nbr.cpu().numpy(), a[("exp", "nbr")])
+    if ("exp", "sorted_keys") in a:
+        np.testing.assert_array_equal(m.keys.cpu().numpy().astype(np.int64), a[("exp", "sorted_keys")])
+
+
+@pytest.mark.parametrize("method", METHODS)
+@pytest.mark.parametrize("workload", ["conv64_f32", "wide128_bf16", "resblock64_bf16", "map512"])
+def test_map_workloads_bit_exact(pkg, dev, workload, method):
+    coords = pkg.workloads.make_coords(workload)
+    batch = int(coords[:, 0].max()) + 1
+    shape = pkg.workloads.grid_shape(workload)
+    m = _build(pkg, dev, coords, batch, shape, method=method)
+    _check(m, coords, batch, shape, (1, 1, 1))
+
+
+@pytest.mark.parametrize("method", METHODS)
+def test_map_edge_cases(pkg, dev, method):
+    # single voxel at the grid corner
+    one = np.array([[0, 0, 0, 0]], np.int32)
+    m = _build(pkg, dev, one, 1, (1, 1, 1), method=method)
+    _check(m, one, 1, (1, 1, 1), (1, 1, 1))
+    # full 3x3x3 block, shuffled, and a full 5x4x6 grid with dilation 2
+    rng = np.random.default_rng(0)
+    block = np.array([[0, x, y, z] for x in range(3) for y in range(3) for z in range(3)], np.int32)
+    block = block[rng.permutation(27)]
+    m = _build(pkg, dev, block, 1, (3, 3, 3), method=method)
+    _check(m, block, 1, (3, 3, 3), (1, 1, 1))
+    full = np.array([[b, x, y, z] for b in range(2) for x in range(5) for y in range(4)
+                     for z in range(6)], np.int32)
+    m = _build(pkg, dev, full, 2, (5, 4, 6), (2, 1, 2), method)
+    _check(m, full, 2, (5, 4, 6), (2, 1, 2))
+    # many samples, non-cubic grid, voxels on every face
+    coords = np.concatenate([
+        np.array([[b, x, y, z] for x in (0, 6) for y in (0, 2, 8) for z in (0, 4)], np.int32)
+        for b in range(7)])
+    m = _build(pkg, dev, coords, 7, (7, 9, 5), method=method)
+    _check(m, coords, 7, (7, 9, 5), (1, 1, 1))
+    # key space above 2^31 cells -> int64 keys
+    big = np.array([[1, 1020, 1023, 1023], [1, 1021, 1023, 1023], [0, 0, 0, 0]], np.int32)
+    m = _build(pkg, dev, big, 3, (1024, 1024, 1024), method=method)
+    assert m.keys.dtype == torch.int64
+    _check(m, big, 3, (1024, 1024, 1024), (1, 1, 1))
+
+
+def test_map_empty(pkg, dev):
+    c = torch.zeros((0, 4), dtype=torch.int32, device=dev)
+    m = pkg.build_neighbor_map(c, (4, 4, 4), 1)
+    assert m.nbr.shape == (0, 27)
+
+
+@pytest.mark.parametrize("method", METHODS)
+def test_map_rejects_duplicates_and_out_of_range(pkg, dev, method):
+    dup = np.array([[0, 1, 1, 1], [0, 2, 2, 2], [0, 1, 1, 1]], np.int32)
+    with pytest.raises(pkg.TscError, match="duplicate"):
+        _build(pkg, dev, dup, 1, (4, 4, 4), method=method)
+    oob = np.array([[0, 1, 1, 1], [0, 4, 0, 0]], np.int32)
+    with pytest.raises(pkg.TscError, match="outside"):
+        _build(pkg, dev, oob, 1, (4, 4, 4), method=method)
+    neg = np.array([[0, 1, -1, 1]], np.int32)
+    with pytest.raises(pkg.TscError, match="outside"):
+        _build(pkg, dev, neg, 1, (4, 4, 4), method=method)
+    # a valid build after the failures still works (status word is cleared per call)
+    ok = np.array([[0, 1, 1, 1], [0, 1, 1, 2]], np.int32)
+    m = _build(pkg, dev, ok, 1, (4, 4, 4), method=method)
+    _check(m, ok, 1, (4, 4, 4), (1, 1, 1))
+
+
+def test_map_rejects_bad_arguments(pkg, dev):
+    c = torch.zeros((2, 4), dtype=torch.int32, device=dev)
+    with pytest.raises(pkg.TscError):
+        pkg.build_neighbor_map(c, (4, 4, 4), 1, kernel_size=(5, 5, 5))
+    with pytest.raises(pkg.TscError):
+        pkg.build_neighbor_map(c, (4, 4, 4), 1, dilation=(0, 1, 1))
+    with pytest.raises(pkg.TscError):
+        pkg.build_neighbor_map(c[:, 1:].contiguous(), (4, 4, 4), 1)

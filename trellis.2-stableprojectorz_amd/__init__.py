@@ -1,0 +1,22 @@
+"""MI355X-native submanifold sparse conv3d for TRELLIS.2 (host side over libtrellis_sparse.so).
+
+Importable under the alias `trellis2_amd` (see __graft_entry__.load_package); the directory name
+is not a Python identifier.
+
+  SparseTensor, SparseConv3d, SparseResBlock3d   operator API of src/sparse (conv3d.ts:18-222)
+  build_neighbor_map, sparse_conv3d,             functional entry points, one C-ABI call each
+  layer_norm, silu, add, sparse_resblock
+  workloads                                      seeded synthetic voxel shells
+"""
+from ._lib import TscError, load_library, header_symbols, LIB_PATH  # noqa: F401
+from .sparse_tensor import SparseTensor, Scale, Fraction, SCALE_IDENTITY, compute_layout  # noqa: F401
+from .conv3d import SparseConv3d, SparseResBlock3d, get_neighbor_map, neighbor_cache_key  # noqa: F401
+from .ops import (NeighborMap, build_neighbor_map, sparse_conv3d, layer_norm, silu, add,  # noqa: F401
+                  sparse_resblock)
+from . import workloads  # noqa: F401
+
+__all__ = [
+    "TscError", "SparseTensor", "SparseConv3d", "SparseResBlock3d", "NeighborMap",
+    "build_neighbor_map", "sparse_conv3d", "layer_norm", "silu", "add", "sparse_resblock",
+    "get_neighbor_map", "neighbor_cache_key", "workloads",
+]

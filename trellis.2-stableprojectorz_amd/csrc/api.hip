@@ -1,0 +1,429 @@
+// C ABI of libtrellis_sparse.so: argument validation, contexts, workspace, error reporting.
+// Validation mirrors what the reference checks before dispatch (src/sparse/ops/conv3d.ts:41-49:
+// GPU input, Ci = weight.shape[4], Co = weight.shape[0]) and adds the checks a C ABI needs
+// (null pointers, alignment, size limits), so bad input becomes a status code, never a fault.
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+
+#include "tsc_internal.h"
+
+namespace tsc {
+
+static thread_local char g_err[512];
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_hip(hipError_t e, const char* what) {
+  if (e == hipSuccess) return TSC_OK;
+  return fail(TSC_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+int workspace(tsc_ctx* ctx, size_t bytes, void** out) {
+  if (bytes <= ctx->ws_bytes) {
+    *out = ctx->ws;
+    return TSC_OK;
+  }
+  // Growing: earlier enqueued work may still use the old block.
+  int st = check_hip(hipStreamSynchronize(ctx->stream), "workspace sync");
+  if (st) return st;
+  if (ctx->ws) {
+    st = check_hip(hipFree(ctx->ws), "workspace free");
+    ctx->ws = nullptr;
+    ctx->ws_bytes = 0;
+    if (st) return st;
+  }
+  size_t want = std::max(bytes + bytes / 4, (size_t)(1u << 20));
+  void* p = nullptr;
+  if (hipMalloc(&p, want) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(TSC_ERR_OOM, "workspace: cannot allocate %zu bytes", want);
+  }
+  ctx->ws = p;
+  ctx->ws_bytes = want;
+  *out = p;
+  return TSC_OK;
+}
+
+void prof_clear(tsc_ctx* ctx) {
+  for (auto& r : ctx->prof) {
+    (void)hipEventDestroy(r.start);
+    (void)hipEventDestroy(r.stop);
+  }
+  ctx->prof.clear();
+}
+
+static bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+static int elem_size(int32_t dtype) {
+  switch (dtype) {
+    case TSC_F32: return 4;
+    case TSC_F16: return 2;
+    case TSC_BF16: return 2;
+  }
+  return 0;
+}
+
+struct DeviceGuard {
+  int prev = -1;
+  explicit DeviceGuard(int dev) {
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    if (prev != dev) (void)hipSetDevice(dev);
+  }
+  ~DeviceGuard() {
+    int cur;
+    if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+  }
+};
+
+static int check_ctx(tsc_ctx* ctx) {
+  if (!ctx) return fail(TSC_ERR_INVALID, "null context");
+  return TSC_OK;
+}
+
+static int validate_conv(tsc_ctx* ctx, int32_t dtype, const void* feats, const void* weight,
+                         const void* bias, const int32_t* nbr, int64_t N, int32_t Ci, int32_t Co,
+                         void* out) {
+  int st = check_ctx(ctx);
+  if (st) return st;
+  const int es = elem_size(dtype);
+  if (!es) return fail(TSC_ERR_INVALID, "conv: unknown dtype %d", dtype);
+  if (N < 0 || N > INT32_MAX) return fail(TSC_ERR_INVALID, "conv: N=%lld out of range", (long long)N);
+  if (Ci <= 0 || Co <= 0) return fail(TSC_ERR_INVALID, "conv: Ci=%d Co=%d must be positive", Ci, Co);
+  if ((Ci * es) % 32 != 0)
+    return fail(TSC_ERR_UNSUPPORTED, "conv: Ci*elem_size=%d bytes must be a multiple of 32", Ci * es);
+  if (Co % 32 != 0) return fail(TSC_ERR_UNSUPPORTED, "conv: Co=%d must be a multiple of 32", Co);
+  if (N == 0) return TSC_OK;
+  if (!feats || !weight || !nbr || !out) return fail(TSC_ERR_INVALID, "conv: null buffer");
+  if (!aligned(feats, 16) || !aligned(weight, 16))
+    return fail(TSC_ERR_INVALID, "conv: feats and weight must be 16-byte aligned");
+  if (!aligned(out, es) || (bias && !aligned(bias, es)))
+    return fail(TSC_ERR_INVALID, "conv: misaligned out/bias");
+  return TSC_OK;
+}
+
+}  // namespace tsc
+
+using namespace tsc;
+
+extern "C" {
+
+int tsc_version(void) { return TSC_VERSION; }
+
+const char* tsc_last_error(void) { return g_err; }
+
+int tsc_ctx_create(int device, void* stream, tsc_ctx** out) {
+  g_err[0] = 0;
+  if (!out) return fail(TSC_ERR_INVALID, "ctx_create: null out");
+  *out = nullptr;
+  int ndev = 0;
+  int st = check_hip(hipGetDeviceCount(&ndev), "hipGetDeviceCount");
+  if (st) return st;
+  if (device < 0 || device >= ndev)
+    return fail(TSC_ERR_INVALID, "ctx_create: device %d not in [0,%d)", device, ndev);
+  DeviceGuard g(device);
+  tsc_ctx* c = new tsc_ctx();
+  c->device = device;
+  c->ws = nullptr;
+  c->ws_bytes = 0;
+  c->stream = (hipStream_t)stream;  // NULL = the HIP null stream
+  *out = c;
+  return TSC_OK;
+}
+
+int tsc_ctx_destroy(tsc_ctx* ctx) {
+  g_err[0] = 0;
+  if (!ctx) return TSC_OK;
+  DeviceGuard g(ctx->device);
+  int st = check_hip(hipStreamSynchronize(ctx->stream), "ctx_destroy sync");
+  if (ctx->ws) (void)hipFree(ctx->ws);
+  prof_clear(ctx);
+  delete ctx;
+  return st;
+}
+
+int tsc_ctx_set_stream(tsc_ctx* ctx, void* stream) {
+  g_err[0] = 0;
+  int st = check_ctx(ctx);
+  if (st) return st;
+  DeviceGuard g(ctx->device);
+  // Work already queued on the old stream may use the workspace: order the new stream after it.
+  if ((hipStream_t)stream != ctx->stream) {
+    st = check_hip(hipStreamSynchronize(ctx->stream), "set_stream sync");
+    if (st) return st;
+  }
+  ctx->stream = (hipStream_t)stream;
+  return TSC_OK;
+}
+
+void* tsc_ctx_stream(tsc_ctx* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
+
+int tsc_sync(tsc_ctx* ctx) {
+  g_err[0] = 0;
+  int st = check_ctx(ctx);
+  if (st) return st;
+  DeviceGuard g(ctx->device);
+  return check_hip(hipStreamSynchronize(ctx->stream), "tsc_sync");
+}
+
+int tsc_malloc(tsc_ctx* ctx, size_t bytes, void** out) {
+  g_err[0] = 0;
+  int st = check_ctx(ctx);
+  if (st) return st;
+  if (!out) return fail(TSC_ERR_INVALID, "malloc: null out");
+  DeviceGuard g(ctx->device);
+  if (hipMalloc(out, bytes ? bytes : 1) != hipSuccess) {
+    (void)hipGetLastError();
+    *out = nullptr;
+    return fail(TSC_ERR_OOM, "malloc: cannot allocate %zu bytes", bytes);
+  }
+  return TSC_OK;
+}
+
+int tsc_free(tsc_ctx* ctx, void* ptr) {
+  g_err[0] = 0;
+  int st = check_ctx(ctx);
+  if (st) return st;
+  if (!ptr) return TSC_OK;
+  DeviceGuard g(ctx->device);
+  st = check_hip(hipStreamSynchronize(ctx->stream), "free sync");
+  if (st) return st;
+  return check_hip(hipFree(ptr), "hipFree");
+}
+
+int tsc_memcpy_h2d(tsc_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  g_err[0] = 0;
+  int st = check_ctx(ctx);
+  if (st) return st;
+  if (!bytes) return TSC_OK;
+  if (!dst || !src) return fail(TSC_ERR_INVALID, "memcpy_h2d: null pointer");
+  DeviceGuard g(ctx->device);
+  st = check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream), "memcpy_h2d");
+  if (st) return st;
+  return check_hip(hipStreamSynchronize(ctx->stream), "memcpy_h2d sync");
+}
+
+int tsc_memcpy_d2h(tsc_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  g_err[0] = 0;
+  int st = check_ctx(ctx);
+  if (st) return st;
+  if (!bytes) return TSC_OK;
+  if (!dst || !src) return fail(TSC_ERR_INVALID, "memcpy_d2h: null pointer");
+  DeviceGuard g(ctx->device);
+  st = check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream), "memcpy_d2h");
+  if (st) return st;
+  return check_hip(hipStreamSynchronize(ctx->stream), "memcpy_d2h sync");
+}
+
+int tsc_memset_zero(tsc_ctx* ctx, void* dst, size_t bytes) {
+  g_err[0] = 0;
+  int st = check_ctx(ctx);
+  if (st) return st;
+  if (!bytes) return TSC_OK;
+  if (!dst) return fail(TSC_ERR_INVALID, "memset_zero: null pointer");
+  DeviceGuard g(ctx->device);
+  return check_hip(hipMemsetAsync(dst, 0, bytes, ctx->stream), "memset_zero");
+}
+
+int tsc_map_key_bytes(int32_t B, int32_t X, int32_t Y, int32_t Z) {
+  if (B <= 0 || X <= 0 || Y <= 0 || Z <= 0) return 0;
+  const int64_t cells = (int64_t)B * X * Y * Z;
+  return cells <= (int64_t(1) << 31) ? 4 : 8;
+}
+
+int tsc_map_build(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t B, int32_t X, int32_t Y,
+                  int32_t Z, const int32_t kernel[3], const int32_t dilation[3], int32_t method,
+                  void* keys_out, int32_t* perm_out, int32_t* nbr_out, uint32_t* status_dev) {
+  g_err[0] = 0;
+  int st = check_ctx(ctx);
+  if (st) return st;
+  if (!kernel || !dilation) return fail(TSC_ERR_INVALID, "map_build: null kernel/dilation");
+  if (kernel[0] != 3 || kernel[1] != 3 || kernel[2] != 3)
+    return fail(TSC_ERR_UNSUPPORTED, "map_build: kernel %dx%dx%d unsupported (3x3x3 only)",
+                kernel[0], kernel[1], kernel[2]);
+  if (dilation[0] < 1 || dilation[1] < 1 || dilation[2] < 1)
+    return fail(TSC_ERR_INVALID, "map_build: dilation must be >= 1");
+  if (N < 0 || N > INT32_MAX) return fail(TSC_ERR_INVALID, "map_build: N=%lld out of range", (long long)N);
+  if (B <= 0 || X <= 0 || Y <= 0 || Z <= 0)
+    return fail(TSC_ERR_INVALID, "map_build: grid %dx%dx%dx%d must be positive", B, X, Y, Z);
+  if (!status_dev) return fail(TSC_ERR_INVALID, "map_build: null status");
+  if (N > 0 && (!coords || !nbr_out)) return fail(TSC_ERR_INVALID, "map_build: null coords/nbr");
+  if (coords && !aligned(coords, 16))
+    return fail(TSC_ERR_INVALID, "map_build: coords must be 16-byte aligned");
+  const int kb = tsc_map_key_bytes(B, X, Y, Z);
+  if (keys_out && !aligned(keys_out, kb)) return fail(TSC_ERR_INVALID, "map_build: misaligned keys");
+  if (method < TSC_MAP_AUTO || method > TSC_MAP_RADIX)
+    return fail(TSC_ERR_INVALID, "map_build: unknown method %d", method);
+  const int64_t cells = (int64_t)B * X * Y * Z;
+  // Bitmap cost is cells/8 bytes to clear and scan; radix sort costs ~32 B/voxel per pass.
+  const int64_t bitmap_bytes = cells / 8;
+  const int64_t kMaxBitmap = int64_t(1) << 33;  // 8 GiB bitmap (2^36 cells)
+  if (method == TSC_MAP_AUTO) method = (bitmap_bytes <= std::max<int64_t>(64 * N, 1 << 24))
+                                           ? TSC_MAP_BITMAP : TSC_MAP_RADIX;
+  if (method == TSC_MAP_BITMAP && bitmap_bytes > kMaxBitmap)
+    return fail(TSC_ERR_UNSUPPORTED, "map_build: grid of %lld cells too large for the bitmap path",
+                (long long)cells);
+  if (cells / 128 >= INT32_MAX) return fail(TSC_ERR_UNSUPPORTED, "map_build: grid too large");
+  DeviceGuard g(ctx->device);
+  if (method == TSC_MAP_RADIX)
+    return map_build_radix(ctx, coords, N, B, X, Y, Z, dilation, keys_out, perm_out, nbr_out,
+                           status_dev);
+  return map_build_bitmap(ctx, coords, N, B, X, Y, Z, dilation, keys_out, perm_out, nbr_out,
+                          status_dev);
+}
+
+int tsc_conv(tsc_ctx* ctx, int32_t dtype, const void* feats, const void* weight, const void* bias,
+             const int32_t* nbr, const int32_t* order, int64_t N, int32_t Ci, int32_t Co,
+             void* out) {
+  return tsc_conv_fused(ctx, dtype, feats, weight, bias, nbr, order, N, Ci, Co, TSC_EPI_BIAS,
+                        nullptr, nullptr, nullptr, 0.f, out);
+}
+
+int tsc_conv_fused(tsc_ctx* ctx, int32_t dtype, const void* feats, const void* weight,
+                   const void* bias, const int32_t* nbr, const int32_t* order, int64_t N,
+                   int32_t Ci, int32_t Co, int32_t epilogue, const void* residual,
+                   const void* ln_gamma, const void* ln_beta, float eps, void* out) {
+  g_err[0] = 0;
+  int st = validate_conv(ctx, dtype, feats, weight, bias, nbr, N, Ci, Co, out);
+  if (st) return st;
+  if (epilogue < TSC_EPI_BIAS || epilogue > TSC_EPI_BIAS_LN_SILU)
+    return fail(TSC_ERR_INVALID, "conv: unknown epilogue %d", epilogue);
+  if (epilogue == TSC_EPI_BIAS_RESIDUAL && N > 0 && !residual)
+    return fail(TSC_ERR_INVALID, "conv: residual epilogue needs a residual buffer");
+  if (N == 0) return TSC_OK;
+  DeviceGuard g(ctx->device);
+  ConvArgs a{dtype, feats, weight, bias, nbr, order, N, Ci, Co,
+             epilogue == TSC_EPI_BIAS_RESIDUAL ? TSC_EPI_BIAS_RESIDUAL : TSC_EPI_BIAS,
+             residual, out};
+  st = conv_launch(ctx, a);
+  if (st || epilogue != TSC_EPI_BIAS_LN_SILU) return st;
+  return layernorm_launch(ctx, dtype, out, N, Co, ln_gamma, ln_beta, eps, 1, out);
+}
+
+int tsc_layernorm(tsc_ctx* ctx, int32_t dtype, const void* x, int64_t N, int32_t C,
+                  const void* gamma, const void* beta, float eps, int32_t apply_silu, void* y) {
+  g_err[0] = 0;
+  int st = check_ctx(ctx);
+  if (st) return st;
+  if (!elem_size(dtype)) return fail(TSC_ERR_INVALID, "layernorm: unknown dtype %d", dtype);
+  if (N < 0 || C <= 0) return fail(TSC_ERR_INVALID, "layernorm: bad shape N=%lld C=%d", (long long)N, C);
+  if (N > 0 && (!x || !y)) return fail(TSC_ERR_INVALID, "layernorm: null buffer");
+  if (!(eps >= 0.f)) return fail(TSC_ERR_INVALID, "layernorm: eps must be >= 0");
+  DeviceGuard g(ctx->device);
+  return layernorm_launch(ctx, dtype, x, N, C, gamma, beta, eps, apply_silu, y);
+}
+
+int tsc_silu(tsc_ctx* ctx, int32_t dtype, const void* x, int64_t numel, void* y) {
+  g_err[0] = 0;
+  int st = check_ctx(ctx);
+  if (st) return st;
+  if (!elem_size(dtype)) return fail(TSC_ERR_INVALID, "silu: unknown dtype %d", dtype);
+  if (numel < 0) return fail(TSC_ERR_INVALID, "silu: negative size");
+  if (numel > 0 && (!x || !y)) return fail(TSC_ERR_INVALID, "silu: null buffer");
+  DeviceGuard g(ctx->device);
+  return silu_launch(ctx, dtype, x, numel, y);
+}
+
+int tsc_add(tsc_ctx* ctx, int32_t dtype, const void* a, const void* b, int64_t numel, void* y) {
+  g_err[0] = 0;
+  int st = check_ctx(ctx);
+  if (st) return st;
+  if (!elem_size(dtype)) return fail(TSC_ERR_INVALID, "add: unknown dtype %d", dtype);
+  if (numel < 0) return fail(TSC_ERR_INVALID, "add: negative size");
+  if (numel > 0 && (!a || !b || !y)) return fail(TSC_ERR_INVALID, "add: null buffer");
+  DeviceGuard g(ctx->device);
+  return add_launch(ctx, dtype, a, b, numel, y);
+}
+
+int tsc_resblock(tsc_ctx* ctx, int32_t dtype, const void* x, const int32_t* nbr,
+                 const int32_t* order, int64_t N, int32_t C, const void* w1, const void* b1,
+                 const void* ln_gamma, const void* ln_beta, float eps, const void* w2,
+                 const void* b2, void* out) {
+  g_err[0] = 0;
+  int st = validate_conv(ctx, dtype, x, w1, b1, nbr, N, C, C, out);
+  if (st) return st;
+  if (N == 0) return TSC_OK;
+  if (!w2) return fail(TSC_ERR_INVALID, "resblock: null w2");
+  if (x == out) return fail(TSC_ERR_INVALID, "resblock: out must not alias x");
+  DeviceGuard g(ctx->device);
+  void* h;
+  st = workspace(ctx, (size_t)N * C * elem_size(dtype), &h);
+  if (st) return st;
+  // h = silu(LN(conv1(x) + b1));  out = x + conv2(h) + b2
+  ConvArgs a1{dtype, x, w1, b1, nbr, order, N, C, C, TSC_EPI_BIAS, nullptr, h};
+  st = conv_launch(ctx, a1);
+  if (st) return st;
+  st = layernorm_launch(ctx, dtype, h, N, C, ln_gamma, ln_beta, eps, 1, h);
+  if (st) return st;
+  ConvArgs a2{dtype, h, w2, b2, nbr, order, N, C, C, TSC_EPI_BIAS_RESIDUAL, x, out};
+  return conv_launch(ctx, a2);
+}
+
+int tsc_profile_enable(tsc_ctx* ctx, int on) {
+  g_err[0] = 0;
+  int st = check_ctx(ctx);
+  if (st) return st;
+  ctx->profile = on != 0;
+  return TSC_OK;
+}
+
+int tsc_profile_collect(tsc_ctx* ctx, int* count) {
+  g_err[0] = 0;
+  int st = check_ctx(ctx);
+  if (st) return st;
+  DeviceGuard g(ctx->device);
+  st = check_hip(hipStreamSynchronize(ctx->stream), "profile sync");
+  if (st) return st;
+  for (auto& r : ctx->prof) {
+    float ms = 0.f;
+    if (hipEventElapsedTime(&ms, r.start, r.stop) != hipSuccess) continue;
+    tsc_prof_agg* a = nullptr;
+    for (auto& e : ctx->prof_agg)
+      if (e.name == r.name) a = &e;
+    if (!a) {
+      ctx->prof_agg.push_back({r.name, 0.0, 0});
+      a = &ctx->prof_agg.back();
+    }
+    a->total_ms += ms;
+    a->launches += 1;
+  }
+  prof_clear(ctx);
+  if (count) *count = (int)ctx->prof_agg.size();
+  return TSC_OK;
+}
+
+int tsc_profile_entry(tsc_ctx* ctx, int index, char* name, int name_len, double* total_ms,
+                      int64_t* launches) {
+  g_err[0] = 0;
+  int st = check_ctx(ctx);
+  if (st) return st;
+  if (index < 0 || index >= (int)ctx->prof_agg.size())
+    return fail(TSC_ERR_INVALID, "profile_entry: index %d out of range", index);
+  const tsc_prof_agg& e = ctx->prof_agg[index];
+  if (name && name_len > 0) snprintf(name, (size_t)name_len, "%s", e.name.c_str());
+  if (total_ms) *total_ms = e.total_ms;
+  if (launches) *launches = e.launches;
+  return TSC_OK;
+}
+
+int tsc_profile_reset(tsc_ctx* ctx) {
+  g_err[0] = 0;
+  int st = check_ctx(ctx);
+  if (st) return st;
+  DeviceGuard g(ctx->device);
+  (void)hipStreamSynchronize(ctx->stream);
+  prof_clear(ctx);
+  ctx->prof_agg.clear();
+  return TSC_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,106 @@
+// Internal declarations shared by the translation units of libtrellis_sparse.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include <string>
+#include <vector>
+
+#include "../../include/tsc.h"
+
+// One kernel launch bracketed by events (recorded only while profiling is on).
+struct tsc_prof_rec {
+  const char* name;
+  hipEvent_t start, stop;
+};
+struct tsc_prof_agg {
+  std::string name;
+  double total_ms;
+  int64_t launches;
+};
+
+struct tsc_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  // Growable device workspace (stream-ordered users; grown only after a stream sync).
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+  bool profile = false;
+  std::vector<tsc_prof_rec> prof;      // pending launches
+  std::vector<tsc_prof_agg> prof_agg;  // aggregated by tsc_profile_collect
+};
+
+namespace tsc {
+
+// Thread-local error string; returns `code` so call sites can `return fail(...)`.
+int fail(int code, const char* fmt, ...);
+int check_hip(hipError_t e, const char* what);
+
+// Ensures ctx->ws holds at least `bytes`; returns TSC_OK or an error status.
+int workspace(tsc_ctx* ctx, size_t bytes, void** out);
+
+void prof_clear(tsc_ctx* ctx);
+
+// Records start/stop events on the context stream around one launch when profiling is on.
+struct ProfScope {
+  tsc_ctx* ctx;
+  tsc_prof_rec rec;
+  bool on;
+  ProfScope(tsc_ctx* c, const char* name) : ctx(c), rec{name, nullptr, nullptr}, on(c->profile) {
+    if (on && (hipEventCreate(&rec.start) != hipSuccess || hipEventCreate(&rec.stop) != hipSuccess ||
+               hipEventRecord(rec.start, ctx->stream) != hipSuccess))
+      on = false;
+  }
+  ~ProfScope() {
+    if (on && hipEventRecord(rec.stop, ctx->stream) == hipSuccess) ctx->prof.push_back(rec);
+  }
+};
+
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Bump allocator over a workspace region (256-byte aligned slices).
+struct Carve {
+  char* base;
+  size_t off;
+  explicit Carve(void* b) : base((char*)b), off(0) {}
+  template <typename T>
+  T* take(size_t count) {
+    T* p = (T*)(base + off);
+    off = align_up(off + count * sizeof(T), 256);
+    return p;
+  }
+};
+
+// ---- launchers implemented in map_build.hip ----
+int map_build_bitmap(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t B, int32_t X,
+                     int32_t Y, int32_t Z, const int32_t dil[3], void* keys_out, int32_t* perm_out,
+                     int32_t* nbr_out, uint32_t* status_dev);
+int map_build_radix(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t B, int32_t X,
+                    int32_t Y, int32_t Z, const int32_t dil[3], void* keys_out, int32_t* perm_out,
+                    int32_t* nbr_out, uint32_t* status_dev);
+
+// ---- launchers implemented in conv.hip ----
+struct ConvArgs {
+  int32_t dtype;
+  const void* feats;
+  const void* weight;
+  const void* bias;      // may be null
+  const int32_t* nbr;
+  const int32_t* order;  // may be null
+  int64_t N;
+  int32_t Ci, Co;
+  int32_t epilogue;      // TSC_EPI_BIAS or TSC_EPI_BIAS_RESIDUAL (LN handled by the caller)
+  const void* residual;  // for TSC_EPI_BIAS_RESIDUAL
+  void* out;
+};
+int conv_launch(tsc_ctx* ctx, const ConvArgs& a);
+
+// ---- launchers implemented in rowops.hip ----
+int layernorm_launch(tsc_ctx* ctx, int32_t dtype, const void* x, int64_t N, int32_t C,
+                     const void* gamma, const void* beta, float eps, int32_t apply_silu, void* y);
+int silu_launch(tsc_ctx* ctx, int32_t dtype, const void* x, int64_t numel, void* y);
+int add_launch(tsc_ctx* ctx, int32_t dtype, const void* a, const void* b, int64_t numel, void* y);
+
+}  // namespace tsc

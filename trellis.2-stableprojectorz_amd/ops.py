@@ -1,0 +1,188 @@
+"""Functional ops over torch device tensors, each one C-ABI call into libtrellis_sparse.so.
+
+torch is used for device memory and the current stream only; all compute is in the HIP library.
+Inputs must be contiguous tensors on a HIP device (there is no CPU path).
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from ._lib import TscError, check
+
+_DTYPES = {torch.float32: _lib.TSC_F32, torch.float16: _lib.TSC_F16, torch.bfloat16: _lib.TSC_BF16}
+
+
+def _code(t: torch.Tensor) -> int:
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError:
+        raise TscError(_lib.TSC_ERR_INVALID, f"unsupported dtype {t.dtype}") from None
+
+
+def _dev(*ts) -> int:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise TscError(_lib.TSC_ERR_INVALID, "tensor is not on a GPU; this path has no CPU fallback")
+        if not t.is_contiguous():
+            raise TscError(_lib.TSC_ERR_INVALID, "tensor must be contiguous")
+        if dev is None:
+            dev = t.device.index
+        elif t.device.index != dev:
+            raise TscError(_lib.TSC_ERR_INVALID, "tensors live on different devices")
+    return dev
+
+
+def _p(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+@dataclass
+class NeighborMap:
+    """Result of the map build: the (N,27) table plus the sorted keys and their rows."""
+
+    nbr: torch.Tensor          # (N,27) int32, original row of each neighbor or -1
+    keys: torch.Tensor         # (N,) int32/int64 sorted unique packed keys
+    perm: torch.Tensor         # (N,) int32, perm[i] = row of keys[i]  (spatially sorted order)
+    spatial_shape: tuple
+    batch_size: int
+    dilation: tuple
+
+
+def build_neighbor_map(coords: torch.Tensor, spatial_shape, batch_size: int,
+                       dilation=(1, 1, 1), kernel_size=(3, 3, 3), method: str = "auto",
+                       validate: bool = True) -> NeighborMap:
+    """Neighbor map of int32 (N,4) [b,x,y,z] coords on the GPU.
+
+    validate=True reads the device status word back (one 4-byte sync) and raises on duplicate or
+    out-of-range coordinates, whose outputs are undefined.
+    """
+    if coords.dtype != torch.int32 or coords.dim() != 2 or coords.shape[1] != 4:
+        raise TscError(_lib.TSC_ERR_INVALID, "coords must be int32 of shape (N,4)")
+    dev = _dev(coords)
+    ctx = _lib.context(dev)
+    n = coords.shape[0]
+    X, Y, Z = (int(s) for s in spatial_shape)
+    kb = ctx.lib.tsc_map_key_bytes(int(batch_size), X, Y, Z)
+    if kb == 0:
+        raise TscError(_lib.TSC_ERR_INVALID, f"bad grid B={batch_size} shape={spatial_shape}")
+    kdt = torch.int32 if kb == 4 else torch.int64
+    nbr = torch.empty((n, 27), dtype=torch.int32, device=coords.device)
+    keys = torch.empty((n,), dtype=kdt, device=coords.device)
+    perm = torch.empty((n,), dtype=torch.int32, device=coords.device)
+    status = torch.empty((1,), dtype=torch.int32, device=coords.device)
+    k = (ctypes.c_int32 * 3)(*kernel_size)
+    d = (ctypes.c_int32 * 3)(*dilation)
+    check(ctx.lib.tsc_map_build(ctx.bind(), _p(coords), n, int(batch_size), X, Y, Z, k, d,
+                                _lib.MAP_METHODS[method], _p(keys), _p(perm), _p(nbr), _p(status)))
+    if validate:
+        st = int(status.item())
+        if st:
+            what = []
+            if st & _lib.TSC_MAP_DUPLICATE:
+                what.append("duplicate coordinates")
+            if st & _lib.TSC_MAP_OUT_OF_RANGE:
+                what.append(f"coordinates outside [0,{batch_size})x[0,{X})x[0,{Y})x[0,{Z})")
+            raise TscError(_lib.TSC_ERR_INVALID, "map build: " + ", ".join(what))
+    return NeighborMap(nbr, keys, perm, (X, Y, Z), int(batch_size), tuple(dilation))
+
+
+def _nbr_and_order(nmap, order):
+    if isinstance(nmap, NeighborMap):
+        return nmap.nbr, (nmap.perm if order is None else order)
+    return nmap, order
+
+
+def sparse_conv3d(feats: torch.Tensor, weight: torch.Tensor, bias, nmap, order=None,
+                  epilogue: str = "bias", residual=None, ln_weight=None, ln_bias=None,
+                  eps: float = 1e-6, out=None) -> torch.Tensor:
+    """out = bias + sum_v feats[nbr[:,v]] @ W[:,v,:]^T  (+ residual | -> LN -> SiLU).
+
+    weight is (Co,Kd,Kh,Kw,Ci) = (Co,3,3,3,Ci), same dtype as feats; accumulation is fp32.
+    nmap is a NeighborMap (its sorted order is used for locality) or an (N,27) int32 table.
+    """
+    nbr, order = _nbr_and_order(nmap, order)
+    if weight.dim() != 5 or tuple(weight.shape[1:4]) != (3, 3, 3):
+        raise TscError(_lib.TSC_ERR_UNSUPPORTED, f"weight must be (Co,3,3,3,Ci), got {tuple(weight.shape)}")
+    co, ci = weight.shape[0], weight.shape[4]
+    n = feats.shape[0]
+    if feats.dim() != 2 or feats.shape[1] != ci:
+        raise TscError(_lib.TSC_ERR_INVALID, f"feats {tuple(feats.shape)} do not match Ci={ci}")
+    if nbr.dtype != torch.int32 or tuple(nbr.shape) != (n, 27):
+        raise TscError(_lib.TSC_ERR_INVALID, "neighbor map must be int32 (N,27)")
+    for t in (weight, bias, residual, ln_weight, ln_bias, out):
+        if t is not None and t.dtype != feats.dtype:
+            raise TscError(_lib.TSC_ERR_INVALID, "all float tensors must share feats' dtype")
+    if bias is not None and bias.numel() != co:
+        raise TscError(_lib.TSC_ERR_INVALID, "bias must have Co elements")
+    if order is not None and (order.dtype != torch.int32 or order.numel() != n):
+        raise TscError(_lib.TSC_ERR_INVALID, "order must be int32 (N,)")
+    epi = {"bias": _lib.TSC_EPI_BIAS, "residual": _lib.TSC_EPI_BIAS_RESIDUAL,
+           "ln_silu": _lib.TSC_EPI_BIAS_LN_SILU}[epilogue]
+    if epi == _lib.TSC_EPI_BIAS_RESIDUAL and (residual is None or tuple(residual.shape) != (n, co)):
+        raise TscError(_lib.TSC_ERR_INVALID, "residual epilogue needs an (N,Co) residual")
+    dev = _dev(feats, weight, bias, nbr, order, residual, ln_weight, ln_bias, out)
+    if out is None:
+        out = torch.empty((n, co), dtype=feats.dtype, device=feats.device)
+    ctx = _lib.context(dev)
+    check(ctx.lib.tsc_conv_fused(ctx.bind(), _code(feats), _p(feats), _p(weight), _p(bias), _p(nbr),
+                                 _p(order), n, ci, co, epi, _p(residual), _p(ln_weight), _p(ln_bias),
+                                 float(eps), _p(out)))
+    return out
+
+
+def layer_norm(x: torch.Tensor, weight=None, bias=None, eps: float = 1e-6, silu: bool = False,
+               out=None) -> torch.Tensor:
+    """Row LayerNorm over the last dim (fp32 math), optionally fused with SiLU."""
+    c = x.shape[-1]
+    rows = x.numel() // c if c else 0
+    dev = _dev(x, weight, bias, out)
+    if out is None:
+        out = torch.empty_like(x)
+    ctx = _lib.context(dev)
+    check(ctx.lib.tsc_layernorm(ctx.bind(), _code(x), _p(x), rows, c,
+                                _p(weight), _p(bias), float(eps), int(silu), _p(out)))
+    return out
+
+
+def silu(x: torch.Tensor, out=None) -> torch.Tensor:
+    dev = _dev(x, out)
+    if out is None:
+        out = torch.empty_like(x)
+    ctx = _lib.context(dev)
+    check(ctx.lib.tsc_silu(ctx.bind(), _code(x), _p(x), x.numel(), _p(out)))
+    return out
+
+
+def add(a: torch.Tensor, b: torch.Tensor, out=None) -> torch.Tensor:
+    if a.shape != b.shape or a.dtype != b.dtype:
+        raise TscError(_lib.TSC_ERR_INVALID, "add: shapes and dtypes must match")
+    dev = _dev(a, b, out)
+    if out is None:
+        out = torch.empty_like(a)
+    ctx = _lib.context(dev)
+    check(ctx.lib.tsc_add(ctx.bind(), _code(a), _p(a), _p(b), a.numel(), _p(out)))
+    return out
+
+
+def sparse_resblock(x: torch.Tensor, nmap, w1, b1, w2, b2, ln_weight=None, ln_bias=None,
+                    eps: float = 1e-6, order=None, out=None) -> torch.Tensor:
+    """out = x + conv2(silu(LN(conv1(x) + b1))) + b2, C = Ci = Co."""
+    nbr, order = _nbr_and_order(nmap, order)
+    n, c = x.shape
+    for w in (w1, w2):
+        if tuple(w.shape) != (c, 3, 3, 3, c) or w.dtype != x.dtype:
+            raise TscError(_lib.TSC_ERR_INVALID, "resblock weights must be (C,3,3,3,C) of x's dtype")
+    dev = _dev(x, nbr, order, w1, b1, w2, b2, ln_weight, ln_bias, out)
+    if out is None:
+        out = torch.empty_like(x)
+    ctx = _lib.context(dev)
+    check(ctx.lib.tsc_resblock(ctx.bind(), _code(x), _p(x), _p(nbr), _p(order), n, c, _p(w1), _p(b1),
+                               _p(ln_weight), _p(ln_bias), float(eps), _p(w2), _p(b2), _p(out)))
+    return out
