@@ -83,7 +83,7 @@ int tsc_memcpy_d2h(tsc_ctx* ctx, void* dst, const void* src, size_t bytes); /* s
 int tsc_memset_zero(tsc_ctx* ctx, void* dst, size_t bytes);               /* stream-ordered */
 
 /* ---- neighbor map ------------------------------------------------------------------------- */
-/* Bytes per packed key: 4 if B*X*Y*Z <= 2^31, else 8.  Keys are key = ((b*X+x)*Y+y)*Z+z. */
+/* Bytes per packed key: 4 if B*X*Y*Z < 2^31, else 8.  Keys are key = ((b*X+x)*Y+y)*Z+z. */
 int tsc_map_key_bytes(int32_t B, int32_t X, int32_t Y, int32_t Z);
 
 /* Build the submanifold neighbor map of a coordinate set.

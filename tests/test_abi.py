@@ -22,8 +22,8 @@ def test_null_context_and_bad_arguments_fail_cleanly(pkg):
     st = lib.tsc_sync(None)
     assert st == 1
     assert lib.tsc_map_key_bytes(1, 512, 512, 512) == 4
-    assert lib.tsc_map_key_bytes(2, 1024, 1024, 1024) == 4  # 2^31 cells: max key 2^31-1
-    assert lib.tsc_map_key_bytes(3, 1024, 1024, 1024) == 8
+    assert lib.tsc_map_key_bytes(2, 1024, 1024, 1023) == 4
+    assert lib.tsc_map_key_bytes(2, 1024, 1024, 1024) == 8  # 2^31 cells
     assert lib.tsc_map_key_bytes(0, 4, 4, 4) == 0
     out = P()
     st = lib.tsc_ctx_create(-1, None, ctypes.byref(out))

@@ -8,7 +8,7 @@ from tests import _golden
 
 pytestmark = pytest.mark.gpu
 
-METHODS = ["bitmap"]
+METHODS = ["bitmap", "radix"]
 
 
 def _build(pkg, dev, coords, batch, shape, dil=(1, 1, 1), method="auto"):
@@ -74,10 +74,10 @@ def test_map_edge_cases(pkg, dev, method):
     m = _build(pkg, dev, coords, 7, (7, 9, 5), method=method)
     _check(m, coords, 7, (7, 9, 5), (1, 1, 1))
     # key space above 2^31 cells -> int64 keys
-    big = np.array([[1, 1020, 1023, 1023], [1, 1021, 1023, 1023], [0, 0, 0, 0]], np.int32)
-    m = _build(pkg, dev, big, 3, (1024, 1024, 1024), method=method)
+    big = np.array([[2, 1020, 1023, 699], [2, 1021, 1023, 699], [0, 0, 0, 0], [1, 5, 5, 5]], np.int32)
+    m = _build(pkg, dev, big, 3, (1024, 1024, 700), method=method)
     assert m.keys.dtype == torch.int64
-    _check(m, big, 3, (1024, 1024, 1024), (1, 1, 1))
+    _check(m, big, 3, (1024, 1024, 700), (1, 1, 1))
 
 
 def test_map_empty(pkg, dev):

@@ -237,7 +237,7 @@ int tsc_memset_zero(tsc_ctx* ctx, void* dst, size_t bytes) {
 int tsc_map_key_bytes(int32_t B, int32_t X, int32_t Y, int32_t Z) {
   if (B <= 0 || X <= 0 || Y <= 0 || Z <= 0) return 0;
   const int64_t cells = (int64_t)B * X * Y * Z;
-  return cells <= (int64_t(1) << 31) ? 4 : 8;
+  return cells < (int64_t(1) << 31) ? 4 : 8;  // int32 keys keep room for a sentinel
 }
 
 int tsc_map_build(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t B, int32_t X, int32_t Y,
@@ -264,12 +264,13 @@ int tsc_map_build(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t B, int
   if (method < TSC_MAP_AUTO || method > TSC_MAP_RADIX)
     return fail(TSC_ERR_INVALID, "map_build: unknown method %d", method);
   const int64_t cells = (int64_t)B * X * Y * Z;
-  // Bitmap cost is cells/8 bytes to clear and scan; radix sort costs ~32 B/voxel per pass.
-  const int64_t bitmap_bytes = cells / 8;
-  const int64_t kMaxBitmap = int64_t(1) << 33;  // 8 GiB bitmap (2^36 cells)
-  if (method == TSC_MAP_AUTO) method = (bitmap_bytes <= std::max<int64_t>(64 * N, 1 << 24))
-                                           ? TSC_MAP_BITMAP : TSC_MAP_RADIX;
-  if (method == TSC_MAP_BITMAP && bitmap_bytes > kMaxBitmap)
+  // The bitmap path streams cells/8 bytes of bitmap three times and keeps a 4 B/cell row table
+  // (touched only at occupied cells); the radix path costs ~100 B/voxel whatever the grid.
+  const int64_t kMaxBitmapCells = int64_t(1) << 32;  // 512 MB bitmap + 16 GB row table
+  if (method == TSC_MAP_AUTO)
+    method = (cells <= std::max<int64_t>(256 * N, int64_t(1) << 24) && cells <= kMaxBitmapCells)
+                 ? TSC_MAP_BITMAP : TSC_MAP_RADIX;
+  if (method == TSC_MAP_BITMAP && cells > kMaxBitmapCells)
     return fail(TSC_ERR_UNSUPPORTED, "map_build: grid of %lld cells too large for the bitmap path",
                 (long long)cells);
   if (cells / 128 >= INT32_MAX) return fail(TSC_ERR_UNSUPPORTED, "map_build: grid too large");

@@ -17,7 +17,7 @@
 
 #include <algorithm>
 
-#include "tsc_internal.h"
+#include "map_common.h"
 
 namespace tsc {
 namespace {
@@ -195,46 +195,38 @@ __global__ void __launch_bounds__(kThreads)
   perm[r] = (int32_t)i;
 }
 
+// Bitmap probe for the column-parallel fill: one 16-byte group load plus its prefix serves the
+// three z taps of a neighbor column (a second group only when a tap crosses a 128-cell
+// boundary); present cells read their original row through perm[rank].
 template <typename K>
-__global__ void __launch_bounds__(kThreads)
-    fill_kernel(const K* __restrict__ keys, const int32_t* __restrict__ perm,
-                const int* __restrict__ count, int32_t X, int32_t Y, int32_t Z, int32_t dD,
-                int32_t dH, int32_t dW, const uint4* __restrict__ bits,
-                const int* __restrict__ prefix, int32_t* __restrict__ nbr) {
-  int64_t i = blockIdx.x * (int64_t)kThreads + threadIdx.x;
-  if (i >= (int64_t)count[0]) return;
-  K key = keys[i];
-  int64_t row = perm[i];
-  K t = key;
-  int32_t z = (int32_t)(t % (K)Z); t /= (K)Z;
-  int32_t y = (int32_t)(t % (K)Y); t /= (K)Y;
-  int32_t x = (int32_t)(t % (K)X);
-  const int64_t YZ = (int64_t)Y * Z;
-  int32_t* dst = nbr + row * 27;
+struct BitmapLookup {
+  const uint4* __restrict__ bits;
+  const int* __restrict__ prefix;
+  const int32_t* __restrict__ perm;
+  __device__ __forceinline__ void column(K kc, K /*column id*/, int32_t z, int32_t Z, int32_t dW,
+                                         int32_t v[3]) const {
+    const int64_t g = (int64_t)(kc >> 7);
+    const uint4 w = bits[g];
+    const int p = prefix[g];
 #pragma unroll
-  for (int kd = 0; kd < 3; ++kd) {
-    int32_t nx = x + (kd - 1) * dD;
-    bool okx = (uint32_t)nx < (uint32_t)X;
-#pragma unroll
-    for (int kh = 0; kh < 3; ++kh) {
-      int32_t ny = y + (kh - 1) * dH;
-      bool okxy = okx && (uint32_t)ny < (uint32_t)Y;
-#pragma unroll
-      for (int kw = 0; kw < 3; ++kw) {
-        int32_t nz = z + (kw - 1) * dW;
-        int32_t val = -1;
-        if (okxy && (uint32_t)nz < (uint32_t)Z) {
-          K nk = (K)((int64_t)key + (int64_t)((kd - 1) * dD) * YZ + (int64_t)((kh - 1) * dH) * Z +
-                     (int64_t)((kw - 1) * dW));
-          bool present;
-          int r = rank_of<K>(nk, bits, prefix, &present);
-          if (present) val = perm[r];
-        }
-        dst[kd * 9 + kh * 3 + kw] = val;
+    for (int kw = 0; kw < 3; ++kw) {
+      const int32_t nz = z + (kw - 1) * dW;
+      if (kw == 1 || (uint32_t)nz >= (uint32_t)Z) continue;  // centre handled below
+      const K kt = (K)((int64_t)kc + (kw - 1) * dW);
+      const int64_t gt = (int64_t)(kt >> 7);
+      uint4 wt = w;
+      int pt = p;
+      if (gt != g) {
+        wt = bits[gt];
+        pt = prefix[gt];
       }
+      const uint32_t word = (uint32_t)(kt >> 5) & 3u, bit = (uint32_t)kt & 31u;
+      if ((pick_word(wt, word) >> bit) & 1u) v[kw] = perm[pt + popc4_below(wt, word, bit)];
     }
+    const uint32_t word = (uint32_t)(kc >> 5) & 3u, bit = (uint32_t)kc & 31u;
+    if ((pick_word(w, word) >> bit) & 1u) v[1] = perm[p + popc4_below(w, word, bit)];
   }
-}
+};
 
 inline unsigned grid_for(int64_t n, int per_block) {
   int64_t b = (n + per_block - 1) / per_block;
@@ -295,8 +287,10 @@ int bitmap_impl(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t B, int32
           (const int4*)coords, N, B, X, Y, Z, bits, prefix, keys, perm);
     }
     ProfScope p(ctx, "map_fill");
-    fill_kernel<K><<<grid_for(N, kThreads), kThreads, 0, s>>>(
-        keys, perm, count, X, Y, Z, dil[0], dil[1], dil[2], bits, prefix, nbr_out);
+    const int32_t per_xcd = mapk::fill_per_xcd(N);
+    mapk::fill_columns_kernel<K, BitmapLookup<K>><<<(unsigned)per_xcd * 8u, mapk::kFillThreads, 0, s>>>(
+        keys, perm, count, 0, (K)-1, X, Y, Z, dil[0], dil[1], dil[2],
+        BitmapLookup<K>{bits, prefix, perm}, per_xcd, nbr_out, nullptr);
   }
   return check_hip(hipGetLastError(), "map_build_bitmap launch");
 }
@@ -307,7 +301,7 @@ int map_build_bitmap(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t B, 
                      int32_t Y, int32_t Z, const int32_t dil[3], void* keys_out, int32_t* perm_out,
                      int32_t* nbr_out, uint32_t* status_dev) {
   const int64_t cells = (int64_t)B * X * Y * Z;
-  if (cells <= (int64_t(1) << 31))
+  if (cells < (int64_t(1) << 31))
     return bitmap_impl<int32_t>(ctx, coords, N, B, X, Y, Z, dil, keys_out, perm_out, nbr_out,
                                 status_dev);
   return bitmap_impl<int64_t>(ctx, coords, N, B, X, Y, Z, dil, keys_out, perm_out, nbr_out,
