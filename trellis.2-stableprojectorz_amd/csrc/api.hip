@@ -99,6 +99,9 @@ static int validate_conv(tsc_ctx* ctx, int32_t dtype, const void* feats, const v
   if (!es) return fail(TSC_ERR_INVALID, "conv: unknown dtype %d", dtype);
   if (N < 0 || N > INT32_MAX) return fail(TSC_ERR_INVALID, "conv: N=%lld out of range", (long long)N);
   if (Ci <= 0 || Co <= 0) return fail(TSC_ERR_INVALID, "conv: Ci=%d Co=%d must be positive", Ci, Co);
+  if ((int64_t)Ci * es > 65536)
+    return fail(TSC_ERR_UNSUPPORTED, "conv: Ci*elem_size=%lld bytes exceeds 65536",
+                (long long)Ci * es);
   if ((Ci * es) % 32 != 0)
     return fail(TSC_ERR_UNSUPPORTED, "conv: Ci*elem_size=%d bytes must be a multiple of 32", Ci * es);
   if (Co % 32 != 0) return fail(TSC_ERR_UNSUPPORTED, "conv: Co=%d must be a multiple of 32", Co);

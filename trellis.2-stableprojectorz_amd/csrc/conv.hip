@@ -8,11 +8,15 @@
 // GEMM view: M = voxel rows (in `order`), N = Co, K = 27 taps x Ci.  A block owns a BM x BN
 // output tile.  It first stages the BM neighbor rows (BM x 27 int32) in LDS and ORs their
 // valid-tap bits: taps that no row of the tile uses are skipped entirely.  The K loop then walks
-// (tap, Ci-chunk) pairs; per chunk every thread issues 16-byte global loads for its share of the
-// gathered A rows (feats[nbr[row,v]], zero when nbr < 0) and of the B rows (W[co, v, ci-chunk],
-// K-contiguous), stores them into a double-buffered, XOR-swizzled LDS tile and the four waves run
-// 32x32 MFMAs over it (v_mfma_f32_32x32x16_{bf16,f16}, v_mfma_f32_32x32x2_f32).  The next chunk's
-// global loads are in flight while the current chunk is multiplied; one barrier per chunk.
+// (tap, Ci-chunk) pairs over XOR-swizzled LDS tiles of gathered A rows (feats[nbr[row,v]], zero
+// when nbr < 0) and K-contiguous B rows (W[co, v, ci-chunk]); four waves run 32x32 MFMAs
+// (v_mfma_f32_32x32x16_{bf16,f16}, v_mfma_f32_32x32x2_f32).  Two pipelines feed the tiles:
+//   conv_mfma_kernel      rows longer than 64 bytes (wide channels, several chunks per tap):
+//                         a 3-8 stage ring filled by direct-to-LDS loads (global_load_lds),
+//                         per-tap source addresses kept in registers, fragments read with
+//                         explicit LDS waits, one block of 4 waves per CU
+//   conv_regstage_kernel  rows of at most 64 bytes (one chunk per tap): register-staged double
+//                         buffer, one barrier per chunk, two blocks per CU
 //
 // MFMA operand layout used (32x32 family): lane l supplies A[i = l%32][k in half l/32] and
 // B[k in half l/32][j = l%32]; accumulator register r of lane l holds
@@ -70,8 +74,307 @@ __device__ __forceinline__ int swz(int row, int part) {
 
 constexpr int kTaps = 27;
 
-template <typename T, int BM, int BN, int KB, int WM, int WN, int EPI>
+// Zeros in device memory: the source of the gathered A pieces whose neighbor is absent (a
+// direct-to-LDS load cannot be told to write zeros).  Rows of up to kZeroBytes bytes: a zero
+// piece advances through it by the same Ci offset as a real feature row.
+constexpr int kZeroBytes = 65536;
+__device__ __attribute__((aligned(16))) uint4 g_zero[kZeroBytes / 16];
+
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+// 32-bit LDS address of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+__device__ __forceinline__ u32x4 lds_read16(uint32_t addr) {
+  u32x4 v;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
+__device__ __forceinline__ int32_t lds_read_i32(const int32_t* p) {
+  int32_t v;
+  asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(lds_addr(p)));
+  return v;
+}
+// Waits for every LDS read issued so far; pin() then ties a value read by asm to this point, so
+// that its uses cannot be scheduled above the wait.
+__device__ __forceinline__ void lds_wait_all() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+template <typename V>
+__device__ __forceinline__ void pin(V& v) {
+  asm volatile("" : "+v"(v));
+}
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// global_load_lds_dwordx4: lane l copies 16 bytes from g to LDS at dst + 16*l (dst is
+// wave-uniform).  The builtin only exists for the device; if it appears in a kernel body that the
+// host pass also parses, clang silently drops the host-side launch stubs, so it lives here with a
+// body compiled in the device pass only.
+__device__ __forceinline__ void lds_dma16(const void* g, lds_ptr_t dst) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_global_load_lds(g, dst, 16, 0, 0);
+#endif
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  // gfx9 s_waitcnt immediate: vmcnt[3:0] | expcnt[6:4] (7 = no wait) | lgkmcnt[11:8] (15 = no
+  // wait) | vmcnt[5:4] at [15:14].
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+template <typename T, int BM, int BN, int KB, int STAGES, int WM, int WN>
 struct ConvCfg {
+  static constexpr int NT = 64 * WM * WN;
+  static constexpr int WAVES = WM * WN;
+  static constexpr int PPR = KB / 16;              // 16-byte pieces per LDS row
+  static constexpr int KC = KB / (int)sizeof(T);   // K elements per chunk
+  static constexpr int EPP = 16 / (int)sizeof(T);  // elements per piece
+  static constexpr int WTM = BM / WM, WTN = BN / WN;
+  static constexpr int FM = WTM / 32, FN = WTN / 32;
+  static constexpr int MS = KB / 32;               // micro-steps per chunk
+  static constexpr int A_PIECES = BM * PPR, B_PIECES = BN * PPR;
+  static constexpr int PIECES = A_PIECES + B_PIECES;  // per stage
+  static constexpr int PPW = PIECES / WAVES;          // pieces per wave per stage
+  static constexpr int IPW = (PPW + 63) / 64;         // load instructions per wave per stage
+  static constexpr int STAGE_BYTES = PIECES * 16;
+  static constexpr int LDE = BN * (int)sizeof(T) + 16;  // epilogue row stride (bytes, padded)
+  static_assert(KB % 32 == 0 && KB <= 128, "chunk must be 32..128 bytes");
+  static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32x32");
+  static_assert(PIECES % WAVES == 0, "every wave issues the same loads");
+  static_assert(STAGES >= 2 && STAGES <= 8, "ring depth");
+  static_assert(IPW * (STAGES - 2) < 64, "vmcnt range");
+};
+
+// Compiler-only memory barrier: keeps LDS accesses on their side of s_barrier without the
+// s_waitcnt vmcnt(0) that a fence would add (that would drain the in-flight ring loads).
+#define TSC_COMPILER_BARRIER() asm volatile("" ::: "memory")
+
+// Submanifold conv tile kernel (see the file comment).  Pipeline per block:
+//   prologue   output rows of the tile (via `order`), their 27 neighbor indices into LDS, OR of
+//              valid-tap bits -> list of the taps any row of the tile uses
+//   main loop  chunks = (used tap, Ci slice of KB bytes).  Chunk c is fetched straight into LDS
+//              ring stage c % STAGES with global_load_lds_dwordx4 (gathered A rows, a zero block
+//              for absent neighbors; K-contiguous weight rows for B), STAGES-1 chunks ahead.
+//              Every wave issues the same IPW loads per chunk, so "chunk c has landed" is the
+//              wave's own s_waitcnt vmcnt(IPW * chunks issued after c) followed by one
+//              s_barrier.  Each stage is a separate LDS array and the loop is unrolled by
+//              STAGES, so the compiler can see which stage a read touches and does not insert
+//              its own vmcnt(0) after the LDS-DMA loads.
+//   epilogue   fp32 accumulators + bias (+ residual) rounded once to T, staged through a padded
+//              LDS tile, written back as 16-byte runs of the scattered output rows.
+template <typename T, int BM, int BN, int KB, int STAGES, int WM, int WN, int EPI>
+__global__ void __launch_bounds__(64 * WM * WN)
+    conv_mfma_kernel(const T* __restrict__ feats, const T* __restrict__ weight,
+                     const T* __restrict__ bias, const int32_t* __restrict__ nbr,
+                     const int32_t* __restrict__ order, int64_t N, int32_t Ci, int32_t Co,
+                     int32_t m_tiles, int32_t n_tiles, int32_t per_xcd, const T* residual,
+                     T* out) {
+  using C = ConvCfg<T, BM, BN, KB, STAGES, WM, WN>;
+  constexpr int SB = C::STAGE_BYTES;
+  __shared__ __attribute__((aligned(16))) unsigned char r0[SB];
+  __shared__ __attribute__((aligned(16))) unsigned char r1[SB];
+  __shared__ __attribute__((aligned(16))) unsigned char r2[STAGES > 2 ? SB : 16];
+  __shared__ __attribute__((aligned(16))) unsigned char r3[STAGES > 3 ? SB : 16];
+  __shared__ __attribute__((aligned(16))) unsigned char r4[STAGES > 4 ? SB : 16];
+  __shared__ __attribute__((aligned(16))) unsigned char r5[STAGES > 5 ? SB : 16];
+  __shared__ __attribute__((aligned(16))) unsigned char r6[STAGES > 6 ? SB : 16];
+  __shared__ __attribute__((aligned(16))) unsigned char r7[STAGES > 7 ? SB : 16];
+  __shared__ __attribute__((aligned(16))) unsigned char sE[BM * C::LDE];
+  __shared__ int32_t sNbr[BM * kTaps];
+  __shared__ int32_t sRow[BM];
+  __shared__ int32_t sTaps[kTaps];
+  __shared__ uint32_t sMask;
+  unsigned char* const ring[8] = {r0, r1, r2, r3, r4, r5, r6, r7};
+
+  // XCD-aware tile order: hardware hands block b to XCD b % 8; give each XCD a contiguous run of
+  // logical tiles, with the n-tiles of one m-tile adjacent, so gathered rows are reused in L2.
+  const int bid = blockIdx.x;
+  const int logical = (bid & 7) * per_xcd + (bid >> 3);
+  if (logical >= m_tiles * n_tiles) return;
+  const int m_tile = logical / n_tiles, n_tile = logical % n_tiles;
+  const int64_t m0 = (int64_t)m_tile * BM;
+  const int n0 = n_tile * BN;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int wm = wid / WN, wn = wid % WN;
+
+  if (tid == 0) sMask = 0u;
+  for (int r = tid; r < BM; r += C::NT) {
+    const int64_t pos = m0 + r;
+    sRow[r] = (pos < N) ? (order ? order[pos] : (int32_t)pos) : -1;
+  }
+  __syncthreads();
+  uint32_t mymask = 0u;
+  for (int j = tid; j < BM * kTaps; j += C::NT) {
+    const int r = j / kTaps, v = j - r * kTaps;
+    const int32_t row = sRow[r];
+    const int32_t s = (row >= 0) ? nbr[(int64_t)row * kTaps + v] : -1;
+    sNbr[j] = s;
+    if (s >= 0) mymask |= 1u << v;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mymask |= __shfl_xor(mymask, off, 64);
+  if (lane == 0 && mymask) atomicOr(&sMask, mymask);
+  __syncthreads();
+  const uint32_t mask = sMask;
+  const int ntaps = __popc(mask);
+  if (tid == 0) {
+    int k = 0;
+    for (uint32_t m = mask; m; m &= m - 1) sTaps[k++] = __ffs(m) - 1;
+  }
+  __syncthreads();
+
+  const int cpt = Ci / C::KC;  // chunks per tap
+  const int nchunks = ntaps * cpt;
+
+  f32x16_t acc[C::FM][C::FN];
+#pragma unroll
+  for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  // Load-issue state.  Chunks are issued in order; whenever the stream enters a new tap, every
+  // lane recomputes the byte address (at ci = 0, swizzle applied) of each piece it fetches:
+  // the gathered feature row (or the zero block when the neighbor is absent) for A pieces, the
+  // weight row W[co, v, :] for B pieces.  Within a tap a chunk only adds its Ci offset.
+  const char* gsrc[C::IPW];
+  int is_tap = -1, is_k = cpt - 1;
+  auto issue = [&](unsigned char* sbase) {
+    if (++is_k == cpt) {
+      is_k = 0;
+      ++is_tap;
+      int v = lds_read_i32(sTaps + is_tap);
+      lds_wait_all();
+      pin(v);
+      int32_t src[C::IPW];
+#pragma unroll
+      for (int j = 0; j < C::IPW; ++j) {
+        const int L = min(wid * C::PPW + j * 64 + lane, C::A_PIECES - 1);
+        src[j] = lds_read_i32(sNbr + (L / C::PPR) * kTaps + v);
+      }
+      lds_wait_all();
+#pragma unroll
+      for (int j = 0; j < C::IPW; ++j) {
+        pin(src[j]);
+        const int L = wid * C::PPW + j * 64 + lane;
+        const bool isA = L < C::A_PIECES;
+        const int La = isA ? L : 0, Lb = isA ? 0 : min(L - C::A_PIECES, C::B_PIECES - 1);
+        const int ra = La / C::PPR, rb = Lb / C::PPR;
+        const char* ga = (src[j] >= 0)
+            ? (const char*)(feats + (int64_t)src[j] * Ci + swz<C::PPR>(ra, La % C::PPR) * C::EPP)
+            : (const char*)g_zero + swz<C::PPR>(ra, La % C::PPR) * 16;
+        const char* gb = (const char*)(weight + ((int64_t)(n0 + rb) * kTaps + v) * Ci +
+                                       swz<C::PPR>(rb, Lb % C::PPR) * C::EPP);
+        gsrc[j] = isA ? ga : gb;
+      }
+    }
+    const int off = is_k * KB;  // bytes into the rows for this chunk's Ci slice
+#pragma unroll
+    for (int j = 0; j < C::IPW; ++j)
+      if (C::PPW % 64 == 0 || j * 64 + lane < C::PPW)
+        lds_dma16(gsrc[j] + off, (lds_ptr_t)(sbase + (wid * C::PPW + j * 64) * 16));
+  };
+
+  // MFMA over one stage.  Fragments are read with inline-asm ds_read_b128 and an explicit
+  // lgkmcnt wait: the compiler sees no LDS read of the ring, so it adds no vmcnt wait for the
+  // DMA loads still in flight into the other stages.
+  auto compute = [&](const unsigned char* sA) {
+    const uint32_t a0 = lds_addr(sA), b0 = a0 + C::A_PIECES * 16;
+#pragma unroll
+    for (int s = 0; s < C::MS; ++s) {
+      const int part = 2 * s + (lane >> 5);
+      u32x4 a[C::FM], b[C::FN];
+#pragma unroll
+      for (int i = 0; i < C::FM; ++i) {
+        const int r = wm * C::WTM + i * 32 + (lane & 31);
+        a[i] = lds_read16(a0 + r * KB + swz<C::PPR>(r, part) * 16);
+      }
+#pragma unroll
+      for (int j = 0; j < C::FN; ++j) {
+        const int r = wn * C::WTN + j * 32 + (lane & 31);
+        b[j] = lds_read16(b0 + r * KB + swz<C::PPR>(r, part) * 16);
+      }
+      lds_wait_all();
+#pragma unroll
+      for (int i = 0; i < C::FM; ++i) pin(a[i]);
+#pragma unroll
+      for (int j = 0; j < C::FN; ++j) pin(b[j]);
+#pragma unroll
+      for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::FN; ++j)
+          mfma_piece<T>(__builtin_bit_cast(uint4, a[i]), __builtin_bit_cast(uint4, b[j]),
+                        acc[i][j]);
+    }
+  };
+
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; ++s)
+    if (s < nchunks) issue(ring[s]);
+  for (int c0 = 0; c0 < nchunks; c0 += STAGES) {
+#pragma unroll
+    for (int s = 0; s < STAGES; ++s) {
+      const int c = c0 + s;
+      if (c < nchunks) {
+        // Chunks issued so far: 0 .. min(nchunks, c + STAGES - 1) - 1; chunk c must be in LDS.
+        const int later = min(nchunks - 1 - c, STAGES - 2);
+        if (later >= STAGES - 2) wait_vmcnt<C::IPW * (STAGES - 2)>();
+        else if (STAGES > 3 && later == 1) wait_vmcnt<C::IPW>();
+        else if (STAGES > 4 && later == 2) wait_vmcnt<C::IPW * 2>();
+        else if (STAGES > 5 && later == 3) wait_vmcnt<C::IPW * 3>();
+        else if (STAGES > 6 && later == 4) wait_vmcnt<C::IPW * 4>();
+        else if (STAGES > 7 && later == 5) wait_vmcnt<C::IPW * 5>();
+        else wait_vmcnt<0>();
+        // Every wave's part of chunk c has landed, and every wave is done reading stage
+        // (c - 1) % STAGES (its MFMAs consumed those LDS reads), which is refilled next.
+        TSC_COMPILER_BARRIER();
+        __builtin_amdgcn_s_barrier();
+        TSC_COMPILER_BARRIER();
+        if (c + STAGES - 1 < nchunks) issue(ring[(s + STAGES - 1) % STAGES]);
+        compute(ring[s]);
+      }
+    }
+  }
+
+  // Epilogue: bias (+ residual) in fp32, one rounding, staged through sE for 16-byte stores.
+#pragma unroll
+  for (int j = 0; j < C::FN; ++j) {
+    const int cl = wn * C::WTN + j * 32 + (lane & 31);
+    const float bv = bias ? to_f32<T>(bias[n0 + cl]) : 0.f;
+#pragma unroll
+    for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int rl = wm * C::WTM + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        float val = acc[i][j][e] + bv;
+        if (EPI == TSC_EPI_BIAS_RESIDUAL) {
+          const int32_t row = sRow[rl];
+          if (row >= 0) val += to_f32<T>(residual[(int64_t)row * Co + n0 + cl]);
+        }
+        *(T*)(sE + rl * C::LDE + cl * (int)sizeof(T)) = from_f32<T>(val);
+      }
+  }
+  __syncthreads();
+  constexpr int PIECES_PER_ROW = BN / C::EPP;
+  for (int q = tid; q < BM * PIECES_PER_ROW; q += C::NT) {
+    const int r = q / PIECES_PER_ROW, pc = q - r * PIECES_PER_ROW;
+    const int32_t row = sRow[r];
+    if (row >= 0)
+      *(uint4*)(out + (int64_t)row * Co + n0 + pc * C::EPP) =
+          *(const uint4*)(sE + r * C::LDE + pc * 16);
+  }
+}
+
+// Register-staged variant for rows of at most 64 bytes (one K chunk per tap, e.g. 32 fp16
+// channels): each thread loads its share of the next chunk into registers while the current
+// chunk is multiplied, then stores it to a double-buffered LDS tile; one barrier per chunk.
+// With a single chunk per tap there is no per-tap address reuse for the direct-to-LDS ring to
+// exploit, and this shorter pipeline (two blocks per CU) keeps more rows in flight.
+template <typename T, int BM, int BN, int KB, int WM, int WN, int EPI>
+struct RegCfg {
   static constexpr int NT = 64 * WM * WN;
   static constexpr int PPR = KB / 16;              // 16-byte pieces per LDS row
   static constexpr int KC = KB / (int)sizeof(T);   // K elements per chunk
@@ -87,12 +390,12 @@ struct ConvCfg {
 
 template <typename T, int BM, int BN, int KB, int WM, int WN, int EPI>
 __global__ void __launch_bounds__(64 * WM * WN)
-    conv_mfma_kernel(const T* __restrict__ feats, const T* __restrict__ weight,
+    conv_regstage_kernel(const T* __restrict__ feats, const T* __restrict__ weight,
                      const T* __restrict__ bias, const int32_t* __restrict__ nbr,
                      const int32_t* __restrict__ order, int64_t N, int32_t Ci, int32_t Co,
                      int32_t m_tiles, int32_t n_tiles, int32_t per_xcd,
                      const T* __restrict__ residual, T* __restrict__ out) {
-  using C = ConvCfg<T, BM, BN, KB, WM, WN, EPI>;
+  using C = RegCfg<T, BM, BN, KB, WM, WN, EPI>;
   __shared__ __attribute__((aligned(16))) unsigned char sA[2][BM * KB];
   __shared__ __attribute__((aligned(16))) unsigned char sB[2][BN * KB];
   __shared__ int32_t sNbr[BM * kTaps];
@@ -248,8 +551,34 @@ __global__ void __launch_bounds__(64 * WM * WN)
   }
 }
 
+
+template <typename T, int BM, int BN, int KB, int WM, int WN, int EPI>
+int launch_reg(tsc_ctx* ctx, const ConvArgs& a) {
+  const int32_t m_tiles = (int32_t)((a.N + BM - 1) / BM);
+  const int32_t n_tiles = a.Co / BN;
+  const int64_t total = (int64_t)m_tiles * n_tiles;
+  const int32_t per_xcd = (int32_t)((total + 7) / 8);
+  const unsigned grid = (unsigned)per_xcd * 8u;
+  static const std::string name = std::string("conv_reg_") +
+      (sizeof(T) == 4 ? "f32" : std::is_same<T, __bf16>::value ? "bf16" : "f16") + "_" +
+      std::to_string(BM) + "x" + std::to_string(BN) + "_k" + std::to_string(KB) +
+      (EPI == TSC_EPI_BIAS_RESIDUAL ? "_res" : "");
+  ProfScope p(ctx, name.c_str());
+  conv_regstage_kernel<T, BM, BN, KB, WM, WN, EPI><<<grid, 64 * WM * WN, 0, ctx->stream>>>(
+      (const T*)a.feats, (const T*)a.weight, (const T*)a.bias, a.nbr, a.order, a.N, a.Ci, a.Co,
+      m_tiles, n_tiles, per_xcd, (const T*)a.residual, (T*)a.out);
+  return check_hip(hipGetLastError(), "conv launch");
+}
+
 template <typename T, int BM, int BN, int KB, int WM, int WN, int EPI>
 int launch_cfg(tsc_ctx* ctx, const ConvArgs& a) {
+  // As many ring stages as fit beside the epilogue tile and the neighbor tile in the 160 KB of
+  // LDS per CU, at most 8.
+  constexpr int STAGE = (BM + BN) * KB;
+  constexpr int FIXED = BM * (BN * (int)sizeof(T) + 16) + BM * kTaps * 4 + BM * 4 + 256;
+  constexpr int FIT = (162816 - FIXED) / STAGE;  // 160 KB of LDS per CU, 1 KB spare
+  constexpr int STAGES = FIT < 8 ? FIT : 8;
+  static_assert(STAGES >= 2, "ring too shallow");
   const int32_t m_tiles = (int32_t)((a.N + BM - 1) / BM);
   const int32_t n_tiles = a.Co / BN;
   const int64_t total = (int64_t)m_tiles * n_tiles;
@@ -257,10 +586,10 @@ int launch_cfg(tsc_ctx* ctx, const ConvArgs& a) {
   const unsigned grid = (unsigned)per_xcd * 8u;
   static const std::string name = std::string("conv_") +
       (sizeof(T) == 4 ? "f32" : std::is_same<T, __bf16>::value ? "bf16" : "f16") + "_" +
-      std::to_string(BM) + "x" + std::to_string(BN) + "_k" + std::to_string(KB) +
-      (EPI == TSC_EPI_BIAS_RESIDUAL ? "_res" : "");
+      std::to_string(BM) + "x" + std::to_string(BN) + "_k" + std::to_string(KB) + "_s" +
+      std::to_string(STAGES) + (EPI == TSC_EPI_BIAS_RESIDUAL ? "_res" : "");
   ProfScope p(ctx, name.c_str());
-  conv_mfma_kernel<T, BM, BN, KB, WM, WN, EPI><<<grid, 64 * WM * WN, 0, ctx->stream>>>(
+  conv_mfma_kernel<T, BM, BN, KB, STAGES, WM, WN, EPI><<<grid, 64 * WM * WN, 0, ctx->stream>>>(
       (const T*)a.feats, (const T*)a.weight, (const T*)a.bias, a.nbr, a.order, a.N, a.Ci, a.Co,
       m_tiles, n_tiles, per_xcd, (const T*)a.residual, (T*)a.out);
   return check_hip(hipGetLastError(), "conv launch");
@@ -276,11 +605,24 @@ inline int pick_kb(int row_bytes) {
 template <typename T, int EPI>
 int dispatch_tiles(tsc_ctx* ctx, const ConvArgs& a) {
   const int kb = pick_kb(a.Ci * (int)sizeof(T));
-  if (a.Co % 128 == 0 && a.Co >= 128) {
-    // Wide channels: 128x128 tile, 2x2 waves of 64x64.
-    if (kb == 128) return launch_cfg<T, 128, 128, 128, 2, 2, EPI>(ctx, a);
-    if (kb == 64) return launch_cfg<T, 128, 128, 64, 2, 2, EPI>(ctx, a);
-    return launch_cfg<T, 128, 128, 32, 2, 2, EPI>(ctx, a);
+  if (a.Ci * (int)sizeof(T) <= 64) {
+    // Narrow input rows: one K chunk per tap -> register-staged double buffer.
+    if (a.Co % 64 == 0) {
+      if (kb == 64) return launch_reg<T, 128, 64, 64, 4, 1, EPI>(ctx, a);
+      return launch_reg<T, 128, 64, 32, 4, 1, EPI>(ctx, a);
+    }
+    if (kb == 64) return launch_reg<T, 128, 32, 64, 4, 1, EPI>(ctx, a);
+    return launch_reg<T, 128, 32, 32, 4, 1, EPI>(ctx, a);
+  }
+  // fp32 tiles stop at 64 columns: a 128x128 fp32 stage plus its epilogue tile leave no room
+  // for a ring of at least two stages in LDS.
+  if constexpr (sizeof(T) < 4) {
+    if (a.Co % 128 == 0) {
+      // Wide channels: 128x128 tile, 2x2 waves of 64x64.
+      if (kb == 128) return launch_cfg<T, 128, 128, 128, 2, 2, EPI>(ctx, a);
+      if (kb == 64) return launch_cfg<T, 128, 128, 64, 2, 2, EPI>(ctx, a);
+      return launch_cfg<T, 128, 128, 32, 2, 2, EPI>(ctx, a);
+    }
   }
   if (a.Co % 64 == 0) {
     // Narrow channels: 128 rows x 64 cols, 4 waves of 32 rows.
