@@ -75,14 +75,58 @@ def kernel_times(ctx, fn, steps: int) -> dict:
     return {k: (ms / n, n / steps) for k, (ms, n) in res.items()}
 
 
-def load_traffic() -> dict:
+# Library profiler names -> the kernel names profiles/traffic.json uses (rocprofv3 symbols
+# shortened by trellis.2-stableprojectorz_amd/profiling.py).
+ROCPROF_NAME = {"map_fill": "fill_columns_kernel<bitmap>", "radix_fill": "fill_columns_kernel<radix>",
+                "map_mark": "mark_kernel<int32>", "map_place": "place_kernel<int32>",
+                "radix_scatter": "scatter_kernel<int32>", "radix_pack": "pack_kernel<int32>"}
+
+
+def load_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` measured by rocprofv3 FETCH_SIZE + WRITE_SIZE runs."""
     p = ROOT / "profiles" / "traffic.json"
-    if p.exists():
-        try:
-            return json.loads(p.read_text())
-        except ValueError:
-            return {}
-    return {}
+    if not p.exists():
+        return None
+    try:
+        doc = json.loads(p.read_text())
+    except ValueError:
+        return None
+    rec = doc.get("kernels", {}).get(ROCPROF_NAME.get(kernel, kernel))
+    if not rec or rec.get("fetch_bytes") is None or rec.get("write_bytes") is None:
+        return None
+    return rec["fetch_bytes"] + rec["write_bytes"]
+
+
+def profile_pass(pkg, dev) -> None:
+    """Short fixed workload for rocprofv3 --pmc runs: a 256 MiB device copy (counter scale),
+    three map builds on map512, and one conv of each conv workload."""
+    import torch
+
+    wl = pkg.workloads
+    c = torch.ones(1 << 26, dtype=torch.int32, device=dev)
+    d = torch.empty_like(c)
+    d.copy_(c)
+    torch.cuda.synchronize()
+    log("calibration copy 256 MiB done")
+    coords = wl.make_coords("map512")
+    cd = torch.from_numpy(coords).to(dev)
+    for _ in range(3):
+        pkg.build_neighbor_map(cd, wl.grid_shape("map512"), 1, validate=False)
+    torch.cuda.synchronize()
+    log("map builds done")
+    dts = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16}
+    for name in ("conv64_f32", "narrow512_f16", "wide128_bf16", "resblock64_bf16"):
+        w = wl.WORKLOADS[name]
+        co_np = coords if w.shell == "map512" else wl.make_coords(name)
+        nmap = pkg.build_neighbor_map(torch.from_numpy(co_np).to(dev), wl.grid_shape(name),
+                                      int(co_np[:, 0].max()) + 1)
+        n = co_np.shape[0]
+        for ci, co in w.channels:
+            f = torch.from_numpy(wl.features(n, ci, 1)).to(dev).to(dts[w.dtype])
+            wt = torch.from_numpy(wl.conv_weight(co, ci, 2)).to(dev).to(dts[w.dtype])
+            pkg.sparse_conv3d(f, wt, None, nmap)
+        torch.cuda.synchronize()
+        log(f"{name} conv done")
 
 
 def cpu_baseline(coords_np, shape, threads: int) -> dict:
@@ -186,6 +230,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
+    ap.add_argument("--profile-pass", action="store_true",
+                    help="run the short fixed workload used for rocprofv3 --pmc runs and exit")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -200,6 +246,9 @@ def main() -> int:
 
     pkg = __graft_entry__.load_package()
     dev = torch.device("cuda:0")
+    if args.profile_pass:
+        profile_pass(pkg, dev)
+        return 0
     wl = pkg.workloads
     t0 = time.time()
     coords = wl.make_coords("map512")
@@ -221,7 +270,7 @@ def main() -> int:
     dom_ms = kt[dom][0]
     per_voxel = MAP_KERNEL_BYTES.get(dom)
     achieved = (per_voxel * n / (dom_ms / 1e3)) if per_voxel else None
-    traffic = load_traffic().get(f"map512/{dom}")
+    traffic = load_traffic(dom)
     roofline = {"kernel": dom, "bound": "hbm",
                 "achieved": round(achieved / 1e9, 1) if achieved else None, "peak": PEAK_HBM / 1e9,
                 "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4) if achieved else None,

@@ -1,0 +1,135 @@
+"""Summaries of rocprofv3 results for profiles/ (reads the rocpd SQLite database rocprofv3 writes).
+
+  python trellis.2-stableprojectorz_amd/profiling.py stats TRACE.db OUT.txt --command "..."
+      per-kernel dispatch count, average / min / max duration and share of GPU time
+  python trellis.2-stableprojectorz_amd/profiling.py traffic FETCH.db WRITE.db OUT.json OUT.txt \
+          --calib-bytes 268435456 --command "..."
+      per-kernel average FETCH_SIZE and WRITE_SIZE (KiB per dispatch) scaled to bytes by the
+      same counters on a device copy of --calib-bytes bytes (the largest copy dispatch in the run)
+
+Kernel names are shortened to the name the library's own profiler uses where possible
+(e.g. conv_mfma_kernel<__bf16,128,128,128,3,2,2,0> -> conv_mfma_kernel<bf16,128x128,k128,s3>).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import re
+import sqlite3
+from collections import defaultdict
+
+_TYPES = {"DF16b": "bf16", "DF16_": "f16", "f": "f32"}
+
+
+def short_name(name: str) -> str:
+    m = re.search(r"(conv_mfma_kernel|conv_regstage_kernel)I(DF16b|DF16_|f)((?:Li\d+E)+)", name)
+    if m:
+        nums = re.findall(r"Li(\d+)E", m.group(3))
+        t = _TYPES[m.group(2)]
+        if m.group(1) == "conv_mfma_kernel":  # BM, BN, KB, STAGES, WM, WN, EPI
+            bm, bn, kb, st, _, _, epi = nums
+            return f"conv_mfma_kernel<{t},{bm}x{bn},k{kb},s{st}{',res' if epi == '1' else ''}>"
+        bm, bn, kb, _, _, epi = nums
+        return f"conv_regstage_kernel<{t},{bm}x{bn},k{kb}{',res' if epi == '1' else ''}>"
+    m = re.search(r"(?:tsc::\(anonymous namespace\)::|N_1\d+)(\w+_kernel)", name)
+    if m:
+        base = m.group(1)
+        tm = re.search(r"<(int|long)", name)
+        if "fill_columns_kernel" in name:
+            base += "<radix>" if "ColumnLookup" in name else "<bitmap>"
+        elif tm:
+            base += f"<{'int32' if tm.group(1) == 'int' else 'int64'}>"
+        return base
+    m = re.search(r"(layernorm\w*_kernel|silu_kernel|add_kernel)", name)
+    if m:
+        return m.group(1)
+    return name[:80]
+
+
+def _rows(db_path: str, sql: str):
+    con = sqlite3.connect(db_path)
+    try:
+        return con.execute(sql).fetchall()
+    finally:
+        con.close()
+
+
+def stats(db: str, out: str, command: str) -> None:
+    agg = defaultdict(list)
+    for name, dur in _rows(db, "select name, duration from kernels"):
+        agg[short_name(name)].append(dur / 1e3)
+    total = sum(sum(v) for v in agg.values()) or 1.0
+    lines = [f"# rocprofv3 kernel trace summary", f"# command: {command}", "",
+             f"{'kernel':58s} {'calls':>6s} {'avg_us':>10s} {'min_us':>10s} {'max_us':>10s} {'share':>7s}"]
+    for k, v in sorted(agg.items(), key=lambda kv: -sum(kv[1])):
+        lines.append(f"{k:58s} {len(v):6d} {sum(v) / len(v):10.2f} {min(v):10.2f} {max(v):10.2f} "
+                     f"{100 * sum(v) / total:6.2f}%")
+    open(out, "w").write("\n".join(lines) + "\n")
+
+
+def _counter(db: str, counter: str):
+    per = defaultdict(list)
+    for name, val, grid in _rows(db, "select kernel_name, value, grid_size from counters_collection "
+                                     f"where counter_name = '{counter}'"):
+        per[name].append((float(val), int(grid)))
+    return per
+
+
+def traffic(fetch_db: str, write_db: str, out_json: str, out_txt: str, calib_bytes: int,
+            command: str) -> None:
+    fetch, write = _counter(fetch_db, "FETCH_SIZE"), _counter(write_db, "WRITE_SIZE")
+
+    def calib(per):
+        copies = [(g, v) for n, vs in per.items() if "copyBuffer" in n for v, g in vs]
+        g, kib = max(copies)  # the largest copy dispatch is the calibration copy
+        return calib_bytes / (kib * 1024.0)
+
+    ff, fw = calib(fetch), calib(write)
+    res = {}
+    for name in sorted(set(fetch) | set(write)):
+        if "copyBuffer" in name or "at::native" in name:
+            continue
+        f = [v for v, _ in fetch.get(name, [])]
+        w = [v for v, _ in write.get(name, [])]
+        key = short_name(name)
+        res[key] = {"fetch_bytes": round(sum(f) / len(f) * 1024 * ff) if f else None,
+                    "write_bytes": round(sum(w) / len(w) * 1024 * fw) if w else None,
+                    "dispatches": len(f)}
+    doc = {"calibration": {"copy_bytes": calib_bytes, "fetch_scale": ff, "write_scale": fw},
+           "kernels": res, "command": command}
+    open(out_json, "w").write(json.dumps(doc, indent=1) + "\n")
+    lines = ["# rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE per dispatch (HBM traffic)",
+             f"# command: {command}",
+             f"# scale: a {calib_bytes} B device copy reads FETCH_SIZE x {ff:.3f} and "
+             f"WRITE_SIZE x {fw:.3f} bytes; both factors applied below", "",
+             f"{'kernel':58s} {'fetch_MB':>10s} {'write_MB':>10s}"]
+    for k, v in res.items():
+        fb = "-" if v["fetch_bytes"] is None else f"{v['fetch_bytes'] / 1e6:10.2f}"
+        wb = "-" if v["write_bytes"] is None else f"{v['write_bytes'] / 1e6:10.2f}"
+        lines.append(f"{k:58s} {fb:>10s} {wb:>10s}")
+    open(out_txt, "w").write("\n".join(lines) + "\n")
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    s = sub.add_parser("stats")
+    s.add_argument("db")
+    s.add_argument("out")
+    s.add_argument("--command", default="")
+    t = sub.add_parser("traffic")
+    t.add_argument("fetch_db")
+    t.add_argument("write_db")
+    t.add_argument("out_json")
+    t.add_argument("out_txt")
+    t.add_argument("--calib-bytes", type=int, default=256 << 20)
+    t.add_argument("--command", default="")
+    a = ap.parse_args()
+    if a.cmd == "stats":
+        stats(a.db, a.out, a.command)
+    else:
+        traffic(a.fetch_db, a.write_db, a.out_json, a.out_txt, a.calib_bytes, a.command)
+
+
+if __name__ == "__main__":
+    main()
