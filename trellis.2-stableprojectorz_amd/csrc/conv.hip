@@ -64,12 +64,15 @@ __device__ __forceinline__ void mfma_piece<float>(const uint4& a, const uint4& b
   acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.w), __uint_as_float(b.w), acc, 0, 0, 0);
 }
 
-// XOR swizzle of 16-byte pieces within an LDS row of PPR pieces, so that the 8 lanes that read
-// one piece column from 8 consecutive rows hit 8 distinct bank groups.
+// XOR swizzle of 16-byte pieces within an LDS row of PPR pieces.  gfx950 LDS has 64 four-byte
+// banks (256 bytes) and serves a ds_read_b128 16 lanes at a time; the MFMA fragment reads have 16
+// consecutive lanes reading one logical piece of 16 consecutive rows.  Rows r and r' share bank
+// groups when (r*PPR*16) mod 256 agrees, i.e. within each residue of r mod (16/PPR); XOR-ing the
+// piece index with (r / (16/PPR)) mod PPR gives those rows distinct pieces -> conflict-free.
 template <int PPR>
 __device__ __forceinline__ int swz(int row, int part) {
-  constexpr int rows_per_128 = (PPR >= 8) ? 1 : 8 / PPR;
-  return part ^ ((row / rows_per_128) % PPR);
+  constexpr int rows_per_256 = 16 / PPR;
+  return part ^ ((row / rows_per_256) % PPR);
 }
 
 constexpr int kTaps = 27;
@@ -124,6 +127,34 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
+// Block -> (row tile, column tile).  The hardware hands block b to XCD b % 8, and each XCD has
+// its own L2.  When the column tiles divide 8, each XCD owns one column tile -- its slice of the
+// weights stays resident in that XCD's L2 -- and a contiguous range of row tiles (rows in
+// spatial order, so gathered neighbor rows are reused there too).  Otherwise each XCD gets a
+// contiguous run of (row, column) tiles with the column tiles of one row tile adjacent.
+// per_xcd = blocks per XCD (grid = 8 * per_xcd), computed by tile_grid() on the host.
+__device__ __forceinline__ bool tile_of(int bid, int m_tiles, int n_tiles, int per_xcd,
+                                        int* m_tile, int* n_tile) {
+  const int xcd = bid & 7, i = bid >> 3;
+  if (8 % n_tiles == 0) {
+    *n_tile = xcd % n_tiles;
+    *m_tile = (xcd / n_tiles) * per_xcd + i;
+    return *m_tile < m_tiles;
+  }
+  const int logical = xcd * per_xcd + i;
+  *m_tile = logical / n_tiles;
+  *n_tile = logical % n_tiles;
+  return logical < m_tiles * n_tiles;
+}
+
+inline int32_t tile_grid_per_xcd(int32_t m_tiles, int32_t n_tiles) {
+  if (8 % n_tiles == 0) {
+    const int32_t groups = 8 / n_tiles;
+    return (m_tiles + groups - 1) / groups;
+  }
+  return (int32_t)(((int64_t)m_tiles * n_tiles + 7) / 8);
+}
+
 template <typename T, int BM, int BN, int KB, int STAGES, int WM, int WN>
 struct ConvCfg {
   static constexpr int NT = 64 * WM * WN;
@@ -140,6 +171,11 @@ struct ConvCfg {
   static constexpr int IPW = (PPW + 63) / 64;         // load instructions per wave per stage
   static constexpr int STAGE_BYTES = PIECES * 16;
   static constexpr int LDE = BN * (int)sizeof(T) + 16;  // epilogue row stride (bytes, padded)
+  // Output rows staged per epilogue pass: a multiple of 32 (one MFMA block) that fits in one
+  // ring stage.
+  static constexpr int EPI_ROWS_FIT = STAGE_BYTES / LDE / 32 * 32;
+  static constexpr int EPI_ROWS = EPI_ROWS_FIT >= BM ? BM : EPI_ROWS_FIT;
+  static_assert(EPI_ROWS >= 32 && BM % EPI_ROWS == 0, "epilogue pass must hold 32-row blocks");
   static_assert(KB % 32 == 0 && KB <= 128, "chunk must be 32..128 bytes");
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32x32");
   static_assert(PIECES % WAVES == 0, "every wave issues the same loads");
@@ -181,19 +217,14 @@ __global__ void __launch_bounds__(64 * WM * WN)
   __shared__ __attribute__((aligned(16))) unsigned char r5[STAGES > 5 ? SB : 16];
   __shared__ __attribute__((aligned(16))) unsigned char r6[STAGES > 6 ? SB : 16];
   __shared__ __attribute__((aligned(16))) unsigned char r7[STAGES > 7 ? SB : 16];
-  __shared__ __attribute__((aligned(16))) unsigned char sE[BM * C::LDE];
   __shared__ int32_t sNbr[BM * kTaps];
   __shared__ int32_t sRow[BM];
   __shared__ int32_t sTaps[kTaps];
   __shared__ uint32_t sMask;
   unsigned char* const ring[8] = {r0, r1, r2, r3, r4, r5, r6, r7};
 
-  // XCD-aware tile order: hardware hands block b to XCD b % 8; give each XCD a contiguous run of
-  // logical tiles, with the n-tiles of one m-tile adjacent, so gathered rows are reused in L2.
-  const int bid = blockIdx.x;
-  const int logical = (bid & 7) * per_xcd + (bid >> 3);
-  if (logical >= m_tiles * n_tiles) return;
-  const int m_tile = logical / n_tiles, n_tile = logical % n_tiles;
+  int m_tile, n_tile;
+  if (!tile_of(blockIdx.x, m_tiles, n_tiles, per_xcd, &m_tile, &n_tile)) return;
   const int64_t m0 = (int64_t)m_tile * BM;
   const int n0 = n_tile * BN;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -339,32 +370,43 @@ __global__ void __launch_bounds__(64 * WM * WN)
     }
   }
 
-  // Epilogue: bias (+ residual) in fp32, one rounding, staged through sE for 16-byte stores.
-#pragma unroll
-  for (int j = 0; j < C::FN; ++j) {
-    const int cl = wn * C::WTN + j * 32 + (lane & 31);
-    const float bv = bias ? to_f32<T>(bias[n0 + cl]) : 0.f;
-#pragma unroll
-    for (int i = 0; i < C::FM; ++i)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int rl = wm * C::WTM + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-        float val = acc[i][j][e] + bv;
-        if (EPI == TSC_EPI_BIAS_RESIDUAL) {
-          const int32_t row = sRow[rl];
-          if (row >= 0) val += to_f32<T>(residual[(int64_t)row * Co + n0 + cl]);
-        }
-        *(T*)(sE + rl * C::LDE + cl * (int)sizeof(T)) = from_f32<T>(val);
-      }
-  }
+  // Epilogue: bias (+ residual) in fp32, one rounding, staged through ring stage 0 (free now) in
+  // passes of RPP rows for 16-byte stores of the scattered output rows.
   __syncthreads();
+  constexpr int RPP = C::EPI_ROWS;
   constexpr int PIECES_PER_ROW = BN / C::EPP;
-  for (int q = tid; q < BM * PIECES_PER_ROW; q += C::NT) {
-    const int r = q / PIECES_PER_ROW, pc = q - r * PIECES_PER_ROW;
-    const int32_t row = sRow[r];
-    if (row >= 0)
-      *(uint4*)(out + (int64_t)row * Co + n0 + pc * C::EPP) =
-          *(const uint4*)(sE + r * C::LDE + pc * 16);
+  unsigned char* sE = r0;
+#pragma unroll
+  for (int p0 = 0; p0 < BM; p0 += RPP) {
+#pragma unroll
+    for (int i = 0; i < C::FM; ++i) {
+      const int rb = wm * C::WTM + i * 32;  // first row of this 32-row fragment block
+      if (rb < p0 || rb >= p0 + RPP) continue;
+#pragma unroll
+      for (int j = 0; j < C::FN; ++j) {
+        const int cl = wn * C::WTN + j * 32 + (lane & 31);
+        const float bv = bias ? to_f32<T>(bias[n0 + cl]) : 0.f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int rl = rb + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+          float val = acc[i][j][e] + bv;
+          if (EPI == TSC_EPI_BIAS_RESIDUAL) {
+            const int32_t row = sRow[rl];
+            if (row >= 0) val += to_f32<T>(residual[(int64_t)row * Co + n0 + cl]);
+          }
+          *(T*)(sE + (rl - p0) * C::LDE + cl * (int)sizeof(T)) = from_f32<T>(val);
+        }
+      }
+    }
+    __syncthreads();
+    for (int q = tid; q < RPP * PIECES_PER_ROW; q += C::NT) {
+      const int r = q / PIECES_PER_ROW, pc = q - r * PIECES_PER_ROW;
+      const int32_t row = sRow[p0 + r];
+      if (row >= 0)
+        *(uint4*)(out + (int64_t)row * Co + n0 + pc * C::EPP) =
+            *(const uint4*)(sE + r * C::LDE + pc * 16);
+    }
+    __syncthreads();
   }
 }
 
@@ -403,12 +445,8 @@ __global__ void __launch_bounds__(64 * WM * WN)
   __shared__ int32_t sTaps[kTaps];
   __shared__ uint32_t sMask;
 
-  // XCD-aware tile order: hardware hands block b to XCD b % 8; give each XCD a contiguous run of
-  // logical tiles, with the n-tiles of one m-tile adjacent, so gathered rows are reused in L2.
-  const int bid = blockIdx.x;
-  const int logical = (bid & 7) * per_xcd + (bid >> 3);
-  if (logical >= m_tiles * n_tiles) return;
-  const int m_tile = logical / n_tiles, n_tile = logical % n_tiles;
+  int m_tile, n_tile;
+  if (!tile_of(blockIdx.x, m_tiles, n_tiles, per_xcd, &m_tile, &n_tile)) return;
   const int64_t m0 = (int64_t)m_tile * BM;
   const int n0 = n_tile * BN;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -556,8 +594,7 @@ template <typename T, int BM, int BN, int KB, int WM, int WN, int EPI>
 int launch_reg(tsc_ctx* ctx, const ConvArgs& a) {
   const int32_t m_tiles = (int32_t)((a.N + BM - 1) / BM);
   const int32_t n_tiles = a.Co / BN;
-  const int64_t total = (int64_t)m_tiles * n_tiles;
-  const int32_t per_xcd = (int32_t)((total + 7) / 8);
+  const int32_t per_xcd = tile_grid_per_xcd(m_tiles, n_tiles);
   const unsigned grid = (unsigned)per_xcd * 8u;
   static const std::string name = std::string("conv_reg_") +
       (sizeof(T) == 4 ? "f32" : std::is_same<T, __bf16>::value ? "bf16" : "f16") + "_" +
@@ -572,17 +609,17 @@ int launch_reg(tsc_ctx* ctx, const ConvArgs& a) {
 
 template <typename T, int BM, int BN, int KB, int WM, int WN, int EPI>
 int launch_cfg(tsc_ctx* ctx, const ConvArgs& a) {
-  // As many ring stages as fit beside the epilogue tile and the neighbor tile in the 160 KB of
-  // LDS per CU, at most 8.
+  // Ring stages: as many as fit beside the neighbor tile in half of the 160 KB of LDS per CU, so
+  // that two blocks (eight waves) share a CU and one block's memory stalls overlap the other's
+  // MFMAs; at most 8.
   constexpr int STAGE = (BM + BN) * KB;
-  constexpr int FIXED = BM * (BN * (int)sizeof(T) + 16) + BM * kTaps * 4 + BM * 4 + 256;
-  constexpr int FIT = (162816 - FIXED) / STAGE;  // 160 KB of LDS per CU, 1 KB spare
+  constexpr int FIXED = BM * kTaps * 4 + BM * 4 + 256;
+  constexpr int FIT = (81408 - FIXED) / STAGE;
   constexpr int STAGES = FIT < 8 ? FIT : 8;
   static_assert(STAGES >= 2, "ring too shallow");
   const int32_t m_tiles = (int32_t)((a.N + BM - 1) / BM);
   const int32_t n_tiles = a.Co / BN;
-  const int64_t total = (int64_t)m_tiles * n_tiles;
-  const int32_t per_xcd = (int32_t)((total + 7) / 8);
+  const int32_t per_xcd = tile_grid_per_xcd(m_tiles, n_tiles);
   const unsigned grid = (unsigned)per_xcd * 8u;
   static const std::string name = std::string("conv_") +
       (sizeof(T) == 4 ? "f32" : std::is_same<T, __bf16>::value ? "bf16" : "f16") + "_" +
@@ -614,25 +651,25 @@ int dispatch_tiles(tsc_ctx* ctx, const ConvArgs& a) {
     if (kb == 64) return launch_reg<T, 128, 32, 64, 4, 1, EPI>(ctx, a);
     return launch_reg<T, 128, 32, 32, 4, 1, EPI>(ctx, a);
   }
-  // fp32 tiles stop at 64 columns: a 128x128 fp32 stage plus its epilogue tile leave no room
-  // for a ring of at least two stages in LDS.
+  // Ring path: chunks of at most 64 bytes, so that a ring of four stages plus the neighbor tile
+  // fit in half of a CU's LDS (two resident blocks).  A 32-byte chunk stage is too small to
+  // stage 32 epilogue rows of a 128-column half tile or a 64-column fp32 tile, so those shapes
+  // take the next narrower tile.
   if constexpr (sizeof(T) < 4) {
-    if (a.Co % 128 == 0) {
+    if (a.Co % 128 == 0 && kb >= 64) {
       // Wide channels: 128x128 tile, 2x2 waves of 64x64.
-      if (kb == 128) return launch_cfg<T, 128, 128, 128, 2, 2, EPI>(ctx, a);
-      if (kb == 64) return launch_cfg<T, 128, 128, 64, 2, 2, EPI>(ctx, a);
-      return launch_cfg<T, 128, 128, 32, 2, 2, EPI>(ctx, a);
+      return launch_cfg<T, 128, 128, 64, 2, 2, EPI>(ctx, a);
     }
-  }
-  if (a.Co % 64 == 0) {
-    // Narrow channels: 128 rows x 64 cols, 4 waves of 32 rows.
-    if (kb == 128) return launch_cfg<T, 128, 64, 128, 4, 1, EPI>(ctx, a);
-    if (kb == 64) return launch_cfg<T, 128, 64, 64, 4, 1, EPI>(ctx, a);
-    return launch_cfg<T, 128, 64, 32, 4, 1, EPI>(ctx, a);
+    if (a.Co % 64 == 0) {
+      // 128 rows x 64 cols, 4 waves of 32 rows.
+      if (kb >= 64) return launch_cfg<T, 128, 64, 64, 4, 1, EPI>(ctx, a);
+      return launch_cfg<T, 128, 64, 32, 4, 1, EPI>(ctx, a);
+    }
+  } else {
+    if (a.Co % 64 == 0 && kb >= 64) return launch_cfg<T, 128, 64, 64, 4, 1, EPI>(ctx, a);
   }
   // Co % 32 == 0
-  if (kb == 128) return launch_cfg<T, 128, 32, 128, 4, 1, EPI>(ctx, a);
-  if (kb == 64) return launch_cfg<T, 128, 32, 64, 4, 1, EPI>(ctx, a);
+  if (kb >= 64) return launch_cfg<T, 128, 32, 64, 4, 1, EPI>(ctx, a);
   return launch_cfg<T, 128, 32, 32, 4, 1, EPI>(ctx, a);
 }
 
