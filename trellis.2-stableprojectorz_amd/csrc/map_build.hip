@@ -289,7 +289,7 @@ int bitmap_impl(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t B, int32
     ProfScope p(ctx, "map_fill");
     const int32_t per_xcd = mapk::fill_per_xcd(N);
     mapk::fill_columns_kernel<K, BitmapLookup<K>><<<(unsigned)per_xcd * 8u, mapk::kFillThreads, 0, s>>>(
-        keys, perm, count, 0, (K)-1, X, Y, Z, dil[0], dil[1], dil[2],
+        keys, perm, count, 0, (K)-1, mapk::KeyCoder<K>::make(X, Y, Z), dil[0], dil[1], dil[2],
         BitmapLookup<K>{bits, prefix, perm}, per_xcd, nbr_out, nullptr);
   }
   return check_hip(hipGetLastError(), "map_build_bitmap launch");

@@ -1,22 +1,22 @@
-// Neighbor-map build by LSD radix sort of packed keys (no global atomics, no grid-sized memsets).
+// Neighbor-map build by radix sort of packed keys (no global atomics, no grid-sized memsets).
 //
 // Same outputs as the bitmap path (sorted unique keys, their rows, the (N,27) neighbor table; see
-// map_build.hip for the semantics and reference citations).  Steps:
-//   pack      coords -> (key, row) in input order; histogram of the first digit per 4096-tile.
-//             Out-of-range coordinates get key = cells (sorts last) and are reported later.
-//   P passes  stable LSD counting sort on D-bit digits (D <= 8, P = ceil(bits/8)):
-//               scan     exclusive scan of the digit-major (digit, tile) histogram
-//               scatter  per tile: wave-ballot multisplit gives each element its stable rank
-//                        among equal digits (one ballot per digit bit -> peer mask -> popcount),
-//                        the tile is reordered by digit in LDS and written as contiguous runs
-//               hist     per-tile histogram of the next digit
-//   columns   col_start[c] = first sorted position whose key >= c*Z, for every (b,x,y) column c;
-//             each block binary-searches its 256 columns inside a range found once per block
-//   fill      per sorted position: 9 neighbor columns -> binary search of the three z taps
-//             inside the column's [start, end) range; present neighbors read perm; duplicate
-//             keys and out-of-range rows set status bits; rows written via LDS staging.
-// When the column table would be much larger than the voxel set (very sparse, huge grids) the
-// fill searches the whole sorted array instead of a column range.
+// map_build.hip for the semantics and reference citations).  Keys have nbits = bitlen(cells-1)
+// bits; the top TB = min(nbits, 10) bits select one of 2^TB buckets.  Steps:
+//   pack       coords -> (key, row) in input order, per-4096-tile histogram of the bucket digit
+//              and a per-tile out-of-range flag.  Out-of-range coordinates are clamped to the
+//              last cell (so every key stays below 2^nbits) and reported through the flag.
+//   scan       exclusive scan over tiles of each bucket's counts (one block per bucket), bucket
+//              totals; block 0 folds the tile flags into the status word.
+//   partition  stable scatter of (key, row) by bucket: wave-ballot multisplit ranks inside a
+//              tile (one ballot per digit bit -> peer mask -> popcount), the tile is reordered
+//              by digit in LDS and written as contiguous runs.
+//   bucket     one block per bucket: stable LSD passes over the bucket's remaining bits (at most
+//              9 per pass) between two L2-resident copies of the bucket, the last pass writing
+//              the outputs; then col_start[c] for the (b,x,y) columns whose first key c*Z falls
+//              in the bucket's key range, by binary search of the sorted bucket in LDS.
+//   fill       window fill from LDS (below), or the column-parallel fill over the whole sorted
+//              array when the column table would be much larger than the voxel set.
 
 #include <algorithm>
 
@@ -29,17 +29,12 @@ constexpr int RT = 256;             // threads per block
 constexpr int RI = 16;              // items per thread
 constexpr int RTILE = RT * RI;      // elements per tile
 constexpr int WAVES = RT / 64;
-constexpr int NBMAX = 256;          // max bins per digit (8-bit digits)
-
-template <typename K>
-__device__ __forceinline__ bool pack_key(int4 c, int32_t B, int32_t X, int32_t Y, int32_t Z,
-                                         K* key) {
-  if ((uint32_t)c.x >= (uint32_t)B || (uint32_t)c.y >= (uint32_t)X ||
-      (uint32_t)c.z >= (uint32_t)Y || (uint32_t)c.w >= (uint32_t)Z)
-    return false;
-  *key = (((K)c.x * X + c.y) * Y + c.z) * Z + c.w;
-  return true;
-}
+constexpr int TBMAX = 10;           // bucket digit bits
+constexpr int NBMAX = 1 << TBMAX;   // buckets
+constexpr int DPT = NBMAX / RT;     // bucket digits owned per thread in the partition prefix
+constexpr int LBITS = 9;            // local pass digit bits
+constexpr int LNB = 1 << LBITS;
+constexpr int LPT = LNB / RT;       // local digits owned per thread
 
 template <typename K>
 __device__ __forceinline__ int digit_of(K k, int shift, int mask) {
@@ -53,45 +48,32 @@ __global__ void clear_status_kernel(uint32_t* status) {
 template <typename K>
 __global__ void __launch_bounds__(RT)
     pack_kernel(const int4* __restrict__ coords, int64_t N, int32_t B, int32_t X, int32_t Y,
-                int32_t Z, K sentinel, K* __restrict__ keys, int32_t* __restrict__ vals, int shift,
-                int dbits, int* __restrict__ counts, int ntiles, uint32_t* __restrict__ status) {
+                int32_t Z, K last_cell, K* __restrict__ keys, int32_t* __restrict__ vals,
+                int shift, int dbits, int* __restrict__ counts, int ntiles,
+                int* __restrict__ oob_tile) {
   __shared__ int hist[NBMAX];
   const int nb = 1 << dbits, mask = nb - 1;
   for (int d = threadIdx.x; d < nb; d += RT) hist[d] = 0;
-  if (blockIdx.x == 0 && threadIdx.x == 0) status[0] = 0u;  // nothing else writes it yet
   __syncthreads();
   const int64_t base = (int64_t)blockIdx.x * RTILE;
+  int oob = 0;
 #pragma unroll 4
   for (int j = 0; j < RI; ++j) {
     const int64_t e = base + j * RT + threadIdx.x;
     if (e < N) {
       K key;
-      if (!pack_key<K>(coords[e], B, X, Y, Z, &key)) key = sentinel;
+      if (!mapk::pack_key<K>(coords[e], B, X, Y, Z, &key)) {
+        key = last_cell;
+        oob = 1;
+      }
       keys[e] = key;
       vals[e] = (int32_t)e;
       atomicAdd(&hist[digit_of<K>(key, shift, mask)], 1);  // LDS atomic
     }
   }
-  __syncthreads();
+  oob = __syncthreads_or(oob);
   for (int d = threadIdx.x; d < nb; d += RT) counts[(int64_t)d * ntiles + blockIdx.x] = hist[d];
-}
-
-template <typename K>
-__global__ void __launch_bounds__(RT)
-    hist_kernel(const K* __restrict__ keys, int64_t N, int shift, int dbits,
-                int* __restrict__ counts, int ntiles) {
-  __shared__ int hist[NBMAX];
-  const int nb = 1 << dbits, mask = nb - 1;
-  for (int d = threadIdx.x; d < nb; d += RT) hist[d] = 0;
-  __syncthreads();
-  const int64_t base = (int64_t)blockIdx.x * RTILE;
-#pragma unroll 4
-  for (int j = 0; j < RI; ++j) {
-    const int64_t e = base + j * RT + threadIdx.x;
-    if (e < N) atomicAdd(&hist[digit_of<K>(keys[e], shift, mask)], 1);
-  }
-  __syncthreads();
-  for (int d = threadIdx.x; d < nb; d += RT) counts[(int64_t)d * ntiles + blockIdx.x] = hist[d];
+  if (threadIdx.x == 0) oob_tile[blockIdx.x] = oob;
 }
 
 __device__ __forceinline__ int wave_incl_scan(int v) {
@@ -104,72 +86,61 @@ __device__ __forceinline__ int wave_incl_scan(int v) {
   return v;
 }
 
-// Block d: exclusive scan over tiles of digit d's counts (in place) and totals[d] = its sum.
-// Coalesced: each round loads 256 consecutive counts, one per thread.
-__global__ void __launch_bounds__(RT)
-    scan_kernel(int* __restrict__ counts, int ntiles, int* __restrict__ totals) {
-  __shared__ int wsum[WAVES];
-  __shared__ int carry_s;
-  int* c = counts + (int64_t)blockIdx.x * ntiles;
+// Exclusive scan of v over the block's threads; *total receives the block sum.
+__device__ __forceinline__ int block_excl_scan(int v, int* wsum, int* total) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  if (threadIdx.x == 0) carry_s = 0;
+  const int incl = wave_incl_scan(v);
+  if (lane == 63) wsum[w] = incl;
   __syncthreads();
+  int pre = incl - v, tot = 0;
+#pragma unroll
+  for (int ww = 0; ww < WAVES; ++ww) {
+    if (ww < w) pre += wsum[ww];
+    tot += wsum[ww];
+  }
+  __syncthreads();
+  *total = tot;
+  return pre;
+}
+
+// Block d: exclusive scan over tiles of bucket d's counts (in place) and totals[d] = its sum.
+// Block 0 also sets the status word from the pack kernel's out-of-range tile flags (the fill
+// adds the duplicate bit later in stream order).
+__global__ void __launch_bounds__(RT)
+    scan_kernel(int* __restrict__ counts, int ntiles, int* __restrict__ totals,
+                const int* __restrict__ oob_tile, uint32_t* __restrict__ status) {
+  __shared__ int wsum[WAVES];
+  int* c = counts + (int64_t)blockIdx.x * ntiles;
+  int carry = 0;
   for (int base = 0; base < ntiles; base += RT) {
     const int i = base + threadIdx.x;
     const int v = (i < ntiles) ? c[i] : 0;
-    const int incl = wave_incl_scan(v);
-    if (lane == 63) wsum[w] = incl;
-    __syncthreads();
-    int pre = carry_s, tot = 0;
-#pragma unroll
-    for (int ww = 0; ww < WAVES; ++ww) {
-      if (ww < w) pre += wsum[ww];
-      tot += wsum[ww];
-    }
-    if (i < ntiles) c[i] = pre + incl - v;
-    __syncthreads();
-    if (threadIdx.x == 0) carry_s += tot;
-    __syncthreads();
+    int tot;
+    const int pre = block_excl_scan(v, wsum, &tot);
+    if (i < ntiles) c[i] = carry + pre;
+    carry += tot;
   }
-  if (threadIdx.x == 0) totals[blockIdx.x] = carry_s;
+  if (threadIdx.x == 0) totals[blockIdx.x] = carry;
+  if (blockIdx.x == 0) {
+    int any = 0;
+    for (int i = threadIdx.x; i < ntiles; i += RT) any |= oob_tile[i];
+    any = __syncthreads_or(any);
+    if (threadIdx.x == 0) status[0] = any ? (uint32_t)TSC_MAP_OUT_OF_RANGE : 0u;
+  }
 }
 
-// One stable counting-sort pass over a tile of RTILE elements.  Wave w owns the contiguous
-// sub-tile [w*RI*64, (w+1)*RI*64) and walks it item by item (lanes = consecutive elements), so
-// element order = (wave, item, lane) and ranks are stable.
-template <typename K>
-__global__ void __launch_bounds__(RT)
-    scatter_kernel(const K* __restrict__ ksrc, const int32_t* __restrict__ vsrc, int64_t N,
-                   int shift, int dbits, const int* __restrict__ offs,
-                   const int* __restrict__ totals, int ntiles,
-                   K* __restrict__ kdst, int32_t* __restrict__ vdst) {
-  __shared__ int wcnt[WAVES][NBMAX];
-  __shared__ int dstart[NBMAX];
-  __shared__ int gbase[NBMAX];
-  __shared__ int wsum[WAVES], gsum[WAVES];
-  __shared__ K sk[RTILE];
-  __shared__ int32_t sv[RTILE];
-  const int nb = 1 << dbits, mask = nb - 1;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  for (int i = tid; i < WAVES * NBMAX; i += RT) (&wcnt[0][0])[i] = 0;
-  __syncthreads();
-  const int64_t tile0 = (int64_t)blockIdx.x * RTILE;
-  const int64_t wbase = tile0 + (int64_t)w * (RI * 64);
+// Stable ranks of one wave's RI items (lanes = consecutive elements, items in order) among equal
+// digits: peers = lanes with the same digit (one ballot per digit bit), rank = popcount of the
+// lower peers + the wave's running count of that digit (cnt, in LDS, advanced by the first peer).
+template <typename K, int N_ITEMS>
+__device__ __forceinline__ void wave_rank(const K (&kk)[N_ITEMS], int64_t first, int64_t limit,
+                                          int shift, int dbits, int* cnt, int (&lr)[N_ITEMS]) {
+  const int lane = threadIdx.x & 63;
+  const int mask = (1 << dbits) - 1;
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  K kk[RI];
-  int32_t vv[RI];
-  int lr[RI];
 #pragma unroll
-  for (int j = 0; j < RI; ++j) {
-    const int64_t e = wbase + j * 64 + lane;
-    const bool valid = e < N;
-    kk[j] = valid ? ksrc[e] : (K)0;
-    vv[j] = valid ? vsrc[e] : 0;
-  }
-#pragma unroll
-  for (int j = 0; j < RI; ++j) {
-    const int64_t e = wbase + j * 64 + lane;
-    const bool valid = e < N;
+  for (int j = 0; j < N_ITEMS; ++j) {
+    const bool valid = first + j * 64 + lane < limit;
     const int d = digit_of<K>(kk[j], shift, mask);
     uint64_t peers = __ballot(valid);
     for (int b = 0; b < dbits; ++b) {
@@ -180,50 +151,79 @@ __global__ void __launch_bounds__(RT)
     lr[j] = 0;
     if (valid) {
       const int before = __popcll(peers & lt_mask);
-      const int cnt = wcnt[w][d];
-      lr[j] = cnt + before;
-      if (before == 0) wcnt[w][d] = cnt + __popcll(peers);
+      const int c = cnt[d];
+      lr[j] = c + before;
+      if (before == 0) cnt[d] = c + __popcll(peers);
     }
   }
+}
+
+// Partition by bucket digit.  Order inside a bucket does not matter (the bucket kernel sorts it
+// completely), so an element's slot among its tile's elements of the same digit comes from an
+// LDS atomic.  The tile is reordered by digit in LDS and written as contiguous runs at
+// (all elements of smaller digits) + (this digit in earlier tiles).
+template <typename K>
+__global__ void __launch_bounds__(RT)
+    partition_kernel(const K* __restrict__ ksrc, const int32_t* __restrict__ vsrc, int64_t N,
+                     int shift, int dbits, const int* __restrict__ offs,
+                     const int* __restrict__ totals, int ntiles, K* __restrict__ kdst,
+                     int32_t* __restrict__ vdst) {
+  __shared__ int lcnt[NBMAX];
+  __shared__ int dstart[NBMAX];
+  __shared__ int gbase[NBMAX];
+  __shared__ int wsum[WAVES];
+  __shared__ K sk[RTILE];
+  __shared__ int32_t sv[RTILE];
+  const int nb = 1 << dbits, mask = nb - 1;
+  const int tid = threadIdx.x;
+  for (int i = tid; i < NBMAX; i += RT) lcnt[i] = 0;
   __syncthreads();
-  // Per digit (thread tid = digit): exclusive prefix over waves, tile total, the tile-local start
-  // of the digit, and its global start = (all elements of smaller digits) + (this digit in
-  // earlier tiles).
-  int tot = 0, gtot = 0;
-  if (tid < nb) {
-    int run = 0;
+  const int64_t tile0 = (int64_t)blockIdx.x * RTILE;
+  K kk[RI];
+  int32_t vv[RI];
+  int slot[RI];
 #pragma unroll
-    for (int ww = 0; ww < WAVES; ++ww) {
-      const int c = wcnt[ww][tid];
-      wcnt[ww][tid] = run;
-      run += c;
-    }
-    tot = run;
-    gtot = totals[tid];
+  for (int j = 0; j < RI; ++j) {
+    const int64_t e = tile0 + j * RT + tid;
+    const bool valid = e < N;
+    kk[j] = valid ? ksrc[e] : (K)0;
+    vv[j] = valid ? vsrc[e] : 0;
   }
-  const int incl = wave_incl_scan(tot);
-  const int gincl = wave_incl_scan(gtot);
-  if (lane == 63) {
-    wsum[w] = incl;
-    gsum[w] = gincl;
+#pragma unroll
+  for (int j = 0; j < RI; ++j) {
+    const int64_t e = tile0 + j * RT + tid;
+    slot[j] = e < N ? atomicAdd(&lcnt[digit_of<K>(kk[j], shift, mask)], 1) : 0;
   }
   __syncthreads();
-  int pre = incl - tot, gpre = gincl - gtot;
-  for (int ww = 0; ww < w; ++ww) {
-    pre += wsum[ww];
-    gpre += gsum[ww];
+  // Thread t owns digits [t*DPT, (t+1)*DPT): tile-local start of each digit and its global start.
+  int loc[DPT];
+  int tsum = 0, gsum = 0;
+#pragma unroll
+  for (int q = 0; q < DPT; ++q) {
+    const int d = tid * DPT + q;
+    loc[q] = lcnt[d];
+    tsum += loc[q];
+    gsum += d < nb ? totals[d] : 0;
   }
-  if (tid < nb) {
-    dstart[tid] = pre;
-    gbase[tid] = gpre + offs[(int64_t)tid * ntiles + blockIdx.x];
+  int dummy;
+  int pre = block_excl_scan(tsum, wsum, &dummy);
+  int gpre = block_excl_scan(gsum, wsum, &dummy);
+#pragma unroll
+  for (int q = 0; q < DPT; ++q) {
+    const int d = tid * DPT + q;
+    dstart[d] = pre;
+    pre += loc[q];
+    if (d < nb) {
+      gbase[d] = gpre + offs[(int64_t)d * ntiles + blockIdx.x];
+      gpre += totals[d];
+    }
   }
   __syncthreads();
 #pragma unroll
   for (int j = 0; j < RI; ++j) {
-    const int64_t e = wbase + j * 64 + lane;
+    const int64_t e = tile0 + j * RT + tid;
     if (e < N) {
-      const int d = digit_of<K>(kk[j], shift, mask);
-      const int p = dstart[d] + wcnt[w][d] + lr[j];
+      const int p = dstart[digit_of<K>(kk[j], shift, mask)] + slot[j];
       sk[p] = kk[j];
       sv[p] = vv[j];
     }
@@ -242,8 +242,7 @@ __global__ void __launch_bounds__(RT)
 
 // First index in [lo, hi) with keys[idx] >= t.
 template <typename K>
-__device__ __forceinline__ int64_t lower_bound(const K* __restrict__ keys, int64_t lo, int64_t hi,
-                                               K t) {
+__device__ __forceinline__ int64_t lower_bound(const K* keys, int64_t lo, int64_t hi, K t) {
   while (lo < hi) {
     const int64_t mid = lo + ((hi - lo) >> 1);
     if (keys[mid] < t) lo = mid + 1;
@@ -252,21 +251,284 @@ __device__ __forceinline__ int64_t lower_bound(const K* __restrict__ keys, int64
   return lo;
 }
 
-// col_start[c] = lower_bound(keys, c*Z) for c in [0, ncol]; blocks own 256 consecutive columns
-// and first bracket their key range with two searches over the whole array.
+// Exclusive scan of the LNB-bin histogram in run[] (in place), LPT bins per thread.
+__device__ __forceinline__ void scan_bins(int* run, int* wsum) {
+  const int tid = threadIdx.x;
+  int c[LPT], sum = 0;
+#pragma unroll
+  for (int q = 0; q < LPT; ++q) {
+    c[q] = run[tid * LPT + q];
+    sum += c[q];
+  }
+  int tot;
+  int pre = block_excl_scan(sum, wsum, &tot);
+#pragma unroll
+  for (int q = 0; q < LPT; ++q) {
+    run[tid * LPT + q] = pre;
+    pre += c[q];
+  }
+}
+
+// wcnt[w][d] (each wave's count of digit d) -> each wave's exclusive offset among the waves;
+// returns the per-thread totals of its LPT digits in cnt.
+__device__ __forceinline__ void wave_offsets(int (*wcnt)[LNB], int (&cnt)[LPT]) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int q = 0; q < LPT; ++q) {
+    const int d = tid * LPT + q;
+    int r = 0;
+#pragma unroll
+    for (int ww = 0; ww < WAVES; ++ww) {
+      const int x = wcnt[ww][d];
+      wcnt[ww][d] = r;
+      r += x;
+    }
+    cnt[q] = r;
+  }
+}
+
+// One block per bucket b (see the file comment).  The bucket occupies [start, start+size) of
+// (k0, v0) after the partition.
+//  * size <= RTILE and lb <= kBitmapBits (every int32-key grid up to 2^27 cells): the bucket is
+//    loaded into LDS once and each element sets bit (key mod 2^lb) of an LDS bitmap of the
+//    bucket's key range; with unique keys, an element's sorted position is the number of set
+//    bits below its own (per-word prefix counts + one popcount).  The sorted bucket is staged in
+//    LDS and stored with coalesced writes.
+//  * size <= RTILE otherwise, or when the bitmap finds a repeated key: stable LSD passes over the
+//    bucket's remaining bits in LDS (histogram of the pass digit, exclusive scan, wave_rank over
+//    wave-contiguous runs, scatter back into LDS), so equal keys end up adjacent for the fill's
+//    duplicate check.
+//  * larger buckets: the same LSD passes through global memory in chunks of RTILE, alternating
+//    between (k0, v0) and (k1, v1), the last pass writing (kout, vout).
+// Then col_start[c] for the columns whose first key c*Z lies in the bucket's key range.
+constexpr int kBitmapBits = 17;
+constexpr int kBitmapWords = (1 << kBitmapBits) / 32;
+
 template <typename K>
-__global__ void __launch_bounds__(RT)
-    columns_kernel(const K* __restrict__ keys, int64_t n, int64_t Z, int64_t ncol,
-                   int32_t* __restrict__ col_start) {
-  __shared__ int64_t range[2];
-  const int64_t c0 = (int64_t)blockIdx.x * RT;
-  if (threadIdx.x < 2) {
-    const int64_t cb = c0 + threadIdx.x * RT;
-    range[threadIdx.x] = (cb > ncol) ? n : lower_bound<K>(keys, 0, n, (K)(cb * Z));
+__device__ __forceinline__ void lsd_pass_lds(K* lk, int32_t* lv, int size, int shift, int dbits,
+                                             int* run, int (*wcnt)[LNB], int* wsum) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int mask = (1 << dbits) - 1;
+  // Wave w ranks elements [w*ipw*64, (w+1)*ipw*64): ipw rows of 64 per wave.
+  const int ipw = ((size + 63) / 64 + WAVES - 1) / WAVES;
+  const int wfirst = w * ipw * 64;
+  const int wlimit = min(size, wfirst + ipw * 64);
+  for (int d = tid; d < LNB; d += RT) run[d] = 0;
+  for (int i = tid; i < WAVES * LNB; i += RT) (&wcnt[0][0])[i] = 0;
+  __syncthreads();
+  for (int i = tid; i < size; i += RT) atomicAdd(&run[digit_of<K>(lk[i], shift, mask)], 1);
+  K kk[RI];
+  int32_t vv[RI];
+  int lr[RI];
+#pragma unroll
+  for (int j = 0; j < RI; ++j) {
+    const int e = wfirst + j * 64 + lane;
+    const bool valid = e < wlimit;
+    kk[j] = valid ? lk[e] : (K)0;
+    vv[j] = valid ? lv[e] : 0;
   }
   __syncthreads();
-  const int64_t c = c0 + threadIdx.x;
-  if (c <= ncol) col_start[c] = (int32_t)lower_bound<K>(keys, range[0], range[1], (K)(c * Z));
+  scan_bins(run, wsum);
+  wave_rank<K, RI>(kk, wfirst, wlimit, shift, dbits, wcnt[w], lr);
+  __syncthreads();
+  int cnt[LPT];
+  wave_offsets(wcnt, cnt);
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < RI; ++j) {
+    const int e = wfirst + j * 64 + lane;
+    if (e < wlimit) {
+      const int d = digit_of<K>(kk[j], shift, mask);
+      const int pos = run[d] + wcnt[w][d] + lr[j];
+      lk[pos] = kk[j];
+      lv[pos] = vv[j];
+    }
+  }
+  __syncthreads();
+}
+
+template <typename K>
+__global__ void __launch_bounds__(RT)
+    bucket_sort_kernel(K* k0, int32_t* v0, K* k1, int32_t* v1, K* __restrict__ kout,
+                       int32_t* __restrict__ vout, const int* __restrict__ totals, int nbk,
+                       int lb, int64_t cells, int64_t Z, int64_t ncol, int64_t n,
+                       int32_t* __restrict__ col_start) {
+  // smem: the key bitmap, or (after it) the LSD digit counters run[LNB] + wcnt[WAVES][LNB].
+  __shared__ uint32_t smem[kBitmapWords];
+  __shared__ uint16_t wpre[kBitmapWords];  // set bits in the words before each word
+  __shared__ int wsum[WAVES];
+  __shared__ K lk[RTILE];
+  __shared__ int32_t lv[RTILE];
+  static_assert(kBitmapWords >= LNB * (WAVES + 1), "LSD counters alias the bitmap");
+  static_assert(RTILE <= 65535, "prefix counts fit 16 bits");
+  uint32_t* bits = smem;
+  int* run = (int*)smem;
+  int(*wcnt)[LNB] = (int(*)[LNB])((int*)smem + LNB);
+  const int tid = threadIdx.x;
+  const int b = blockIdx.x;
+  int part = 0;
+  for (int d = tid; d < b; d += RT) part += totals[d];
+  int start32;
+  (void)block_excl_scan(part, wsum, &start32);
+  const int64_t start = start32;
+  const int size = totals[b];
+  const bool fits = size <= RTILE;
+  const int passes = (lb + LBITS - 1) / LBITS;
+  const int pbits = passes ? (lb + passes - 1) / passes : 0;
+
+  if (fits) {
+    for (int i = tid; i < size; i += RT) {
+      lk[i] = k0[start + i];
+      lv[i] = v0[start + i];
+    }
+    bool sorted = passes == 0;
+    if (!sorted && lb <= kBitmapBits) {
+      const int nwords = ((1 << lb) + 31) / 32;
+      const K lmask = (K)((1u << lb) - 1u);
+      for (int i = tid; i < nwords; i += RT) bits[i] = 0u;
+      __syncthreads();
+      K kk[RI];
+      int32_t vv[RI];
+      int loc[RI];
+      int dup = 0;
+#pragma unroll
+      for (int j = 0; j < RI; ++j) {
+        const int i = j * RT + tid;
+        if (i < size) {
+          kk[j] = lk[i];
+          vv[j] = lv[i];
+          loc[j] = (int)(kk[j] & lmask);
+          const uint32_t bit = 1u << (loc[j] & 31);
+          dup |= (atomicOr(&bits[loc[j] >> 5], bit) & bit) != 0u;
+        }
+      }
+      dup = __syncthreads_or(dup);
+      if (!dup) {
+        // Per-word prefix counts: thread t owns words [t*wpt, (t+1)*wpt).
+        const int wpt = (nwords + RT - 1) / RT;
+        int sum = 0;
+        for (int q = 0; q < wpt; ++q) {
+          const int wi = tid * wpt + q;
+          if (wi < nwords) sum += __popc(bits[wi]);
+        }
+        int tot;
+        int pre = block_excl_scan(sum, wsum, &tot);
+        for (int q = 0; q < wpt; ++q) {
+          const int wi = tid * wpt + q;
+          if (wi < nwords) {
+            wpre[wi] = (uint16_t)pre;
+            pre += __popc(bits[wi]);
+          }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < RI; ++j) {
+          const int i = j * RT + tid;
+          if (i < size) {
+            const int wi = loc[j] >> 5;
+            const int r = wpre[wi] + __popc(bits[wi] & ((1u << (loc[j] & 31)) - 1u));
+            lk[r] = kk[j];
+            lv[r] = vv[j];
+          }
+        }
+        sorted = true;
+      }
+      __syncthreads();
+    }
+    if (!sorted) {
+      for (int p = 0; p < passes; ++p) {
+        const int shift = p * pbits;
+        lsd_pass_lds<K>(lk, lv, size, shift, min(pbits, lb - shift), run, wcnt, wsum);
+      }
+    }
+    __syncthreads();
+    for (int i = tid; i < size; i += RT) {
+      kout[start + i] = lk[i];
+      vout[start + i] = lv[i];
+    }
+  } else {
+    for (int p = 0; p < passes; ++p) {
+      const int shift = p * pbits;
+      const int dbits = min(pbits, lb - shift);
+      const int mask = (1 << dbits) - 1;
+      const bool last = p == passes - 1;
+      const K* ks = (p & 1) ? k1 : k0;
+      const int32_t* vs = (p & 1) ? v1 : v0;
+      K* kd = last ? kout : ((p & 1) ? k0 : k1);
+      int32_t* vd = last ? vout : ((p & 1) ? v0 : v1);
+      const int lane = tid & 63, w = tid >> 6;
+      for (int d = tid; d < LNB; d += RT) run[d] = 0;
+      __syncthreads();
+      for (int i = tid; i < size; i += RT)
+        atomicAdd(&run[digit_of<K>(ks[start + i], shift, mask)], 1);
+      __syncthreads();
+      scan_bins(run, wsum);
+      for (int c0 = 0; c0 < size; c0 += RTILE) {
+        for (int i = tid; i < WAVES * LNB; i += RT) (&wcnt[0][0])[i] = 0;
+        __syncthreads();
+        const int wfirst = c0 + w * (RI * 64);
+        const int wlimit = min(size, wfirst + RI * 64);
+        K kk[RI];
+        int32_t vv[RI];
+        int lr[RI];
+#pragma unroll
+        for (int j = 0; j < RI; ++j) {
+          const int e = wfirst + j * 64 + lane;
+          const bool valid = e < wlimit;
+          kk[j] = valid ? ks[start + e] : (K)0;
+          vv[j] = valid ? vs[start + e] : 0;
+        }
+        wave_rank<K, RI>(kk, wfirst, wlimit, shift, dbits, wcnt[w], lr);
+        __syncthreads();
+        int cnt[LPT];
+        wave_offsets(wcnt, cnt);
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < RI; ++j) {
+          const int e = wfirst + j * 64 + lane;
+          if (e < wlimit) {
+            const int d = digit_of<K>(kk[j], shift, mask);
+            const int pos = run[d] + wcnt[w][d] + lr[j];
+            kd[start + pos] = kk[j];
+            vd[start + pos] = vv[j];
+          }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < LPT; ++q) run[tid * LPT + q] += cnt[q];
+        __syncthreads();
+      }
+    }
+    if (passes == 0) {
+      for (int i = tid; i < size; i += RT) {
+        kout[start + i] = k0[start + i];
+        vout[start + i] = v0[start + i];
+      }
+    }
+  }
+  if (!col_start) return;
+  __syncthreads();
+  // Columns whose first key c*Z lies in this bucket's key range [b << lb, (b+1) << lb).
+  const int64_t key_lo = (int64_t)b << lb;
+  const int64_t key_hi = std::min<int64_t>((int64_t)(b + 1) << lb, cells);
+  const int64_t c_lo = (key_lo + Z - 1) / Z, c_hi = (key_hi + Z - 1) / Z;
+  for (int64_t c = c_lo + tid; c < c_hi; c += RT) {
+    const K t = (K)(c * Z);
+    int64_t pos;
+    if (fits) {
+      int lo = 0, hi = size;
+      while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (lk[mid] < t) lo = mid + 1;
+        else hi = mid;
+      }
+      pos = lo;
+    } else {
+      pos = lower_bound<K>(kout + start, 0, size, t);
+    }
+    col_start[c] = (int32_t)(start + pos);
+  }
+  if (b == nbk - 1 && tid == 0) col_start[ncol] = (int32_t)n;
 }
 
 // Column-index probe for the column-parallel fill: the neighbor column's keys occupy
@@ -299,6 +561,143 @@ struct ColumnLookup {
   }
 };
 
+// Window fill: a block owns kWinVox consecutive sorted voxels.  Their columns span
+// [c_first, c_last]; every neighbor column with offset (kd-1)*dD along x lies in
+// [c_first + (kd-1)*dD*Y - dH, c_last + (kd-1)*dD*Y + dH], and the sorted voxels of those
+// columns are one contiguous run of the sorted arrays.  Phase 1 copies, per kd, that run's z
+// values and rows plus the column starts into LDS with coalesced loads; phase 2 resolves every
+// probe from LDS (9 lanes per voxel as in the column-parallel fill), so the only global traffic
+// left per probe is the 12-byte row write.  A kd window that does not fit (very sparse or very
+// dense regions) falls back to the global column lookup for that kd only.
+constexpr int kWinThreads = 256;
+constexpr int kWinRounds = 8;
+constexpr int kWinVox = kWinRounds * mapk::kFillVoxPerWave * (kWinThreads / 64);  // 224
+constexpr int kWinCapE = 512;  // voxels per kd window
+constexpr int kWinCapC = 512;  // columns per kd window (LDS ~20 KB per block: 8 blocks per CU)
+
+template <typename K>
+__global__ void __launch_bounds__(kWinThreads)
+    fill_window_kernel(const K* __restrict__ keys, const int32_t* __restrict__ perm,
+                       const int32_t* __restrict__ col_start, int64_t n, K sentinel,
+                       mapk::KeyCoder<K> kc_, int32_t dD, int32_t dH, int32_t dW, int64_t ncol,
+                       int32_t per_xcd, int32_t* __restrict__ nbr, uint32_t* __restrict__ status) {
+  __shared__ int32_t lz[3][kWinCapE];
+  __shared__ int32_t lp[3][kWinCapE];
+  __shared__ int32_t lcs[3][kWinCapC + 1];
+  __shared__ int64_t w_lo[3];
+  __shared__ int32_t w_e0[3], w_ne[3], w_nc[3];
+  __shared__ int64_t c_range[2];
+  __shared__ K sk[kWinVox + 1];  // sk[0] = key before the block (duplicate check)
+  __shared__ int32_t sp[kWinVox];
+  const int tid = threadIdx.x;
+  const int32_t X = kc_.X, Y = kc_.Y, Z = kc_.Z;
+  const int64_t logical = (int64_t)(blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+  const int64_t i0 = logical * kWinVox;
+  if (i0 >= n) return;  // uniform per block
+  const int64_t i1 = (i0 + kWinVox < n) ? i0 + kWinVox : n;
+  const int nv = (int)(i1 - i0);
+  if (tid < 2) {
+    const K k = keys[tid == 0 ? i0 : i1 - 1];
+    const int64_t c = (int64_t)kc_.column_of(k);
+    c_range[tid] = c < ncol ? c : ncol - 1;  // the sentinel key maps past the last column
+  }
+  for (int j = tid; j <= nv; j += kWinThreads) {
+    const int64_t e = i0 - 1 + j;
+    sk[j] = e >= 0 ? keys[e] : (K)-1;
+    if (j > 0) sp[j - 1] = perm[e];
+  }
+  __syncthreads();
+  if (tid < 3) {
+    const int64_t shiftc = (int64_t)(tid - 1) * dD * Y;
+    int64_t lo = c_range[0] + shiftc - dH, hi = c_range[1] + shiftc + dH;
+    if (lo < 0) lo = 0;
+    if (hi > ncol - 1) hi = ncol - 1;
+    int32_t e0 = 0, ne = 0, nc = 0;
+    if (lo <= hi && hi - lo + 1 <= kWinCapC) {
+      e0 = col_start[lo];
+      ne = col_start[hi + 1] - e0;
+      nc = (int32_t)(hi - lo + 1);
+      if (ne > kWinCapE) nc = -1;
+    } else if (lo <= hi) {
+      nc = -1;
+    }
+    w_lo[tid] = lo;
+    w_e0[tid] = e0;
+    w_ne[tid] = ne;
+    w_nc[tid] = nc;  // -1: window does not fit, probes of this kd go to global memory
+  }
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < 3; ++w) {
+    const int nc = w_nc[w];
+    if (nc <= 0) continue;
+    const int64_t lo = w_lo[w];
+    const int32_t e0 = w_e0[w], ne = w_ne[w];
+    for (int j = tid; j <= nc; j += kWinThreads) lcs[w][j] = col_start[lo + j] - e0;
+    for (int j = tid; j < ne; j += kWinThreads) {
+      lz[w][j] = kc_.z_of(keys[e0 + j]);
+      lp[w][j] = perm[e0 + j];
+    }
+  }
+  __syncthreads();
+
+  const int lane = tid & 63, wid = tid >> 6;
+  const int slot = lane / mapk::kFillLanes, col = lane - slot * mapk::kFillLanes;
+  if (slot >= mapk::kFillVoxPerWave) return;
+  const int kd = col / 3, kh = col - kd * 3;
+  const int nc_w = w_nc[kd];
+  const int64_t lo_w = w_lo[kd];
+  ColumnLookup<K, true> glk{keys, col_start, perm, n};
+  for (int r = 0; r < kWinRounds; ++r) {
+    const int li = (wid * kWinRounds + r) * mapk::kFillVoxPerWave + slot;
+    if (li >= nv) break;
+    const K key = sk[li + 1];
+    if (key == sentinel) {  // out-of-range voxel: reported, no row written
+      if (col == 0) atomicOr(status, TSC_MAP_OUT_OF_RANGE);
+      continue;
+    }
+    if (col == 0 && sk[li] == key) atomicOr(status, TSC_MAP_DUPLICATE);
+    const int32_t row = sp[li];
+    K column;
+    int32_t x, y, z;
+    kc_.decode(key, &column, &x, &y, &z);
+    const int32_t nx = x + (kd - 1) * dD, ny = y + (kh - 1) * dH;
+    int32_t v[3] = {-1, -1, -1};
+    if ((uint32_t)nx < (uint32_t)X && (uint32_t)ny < (uint32_t)Y) {
+      const int64_t ncl = (int64_t)column + (int64_t)(kd - 1) * dD * Y + (kh - 1) * dH;
+      if (nc_w > 0) {
+        const int j = (int)(ncl - lo_w);
+        int a = lcs[kd][j];
+        const int e = lcs[kd][j + 1];
+        const bool has_lo = z - dW >= 0, has_hi = z + dW < Z;
+        const int32_t first = has_lo ? z - dW : z, last = has_hi ? z + dW : z;
+        int b = e;
+        while (a < b) {  // first entry with z >= first
+          const int mid = (a + b) >> 1;
+          if (lz[kd][mid] < first) a = mid + 1;
+          else b = mid;
+        }
+        for (; a < e; ++a) {
+          const int32_t zz = lz[kd][a];
+          if (zz > last) break;
+          if (zz == z) v[1] = lp[kd][a];
+          else if (has_lo && zz == z - dW) v[0] = lp[kd][a];
+          else if (has_hi && zz == z + dW) v[2] = lp[kd][a];
+        }
+      } else {
+        const K kc = (K)((int64_t)key + (int64_t)((kd - 1) * dD) * ((int64_t)Y * Z) +
+                         (int64_t)((kh - 1) * dH) * Z);
+        glk.column(kc, (K)ncl, z, Z, dW, v);
+      }
+    }
+    if (col == 4) v[1] = row;  // tap 13 is the voxel itself
+    int32_t* dst = nbr + (int64_t)row * 27 + col * 3;
+    dst[0] = v[0];
+    dst[1] = v[1];
+    dst[2] = v[2];
+  }
+}
+
 inline int bit_length(uint64_t v) {
   int b = 0;
   while (v) {
@@ -313,16 +712,18 @@ int radix_impl(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t B, int32_
                int32_t Z, const int32_t dil[3], void* keys_out, int32_t* perm_out,
                int32_t* nbr_out, uint32_t* status_dev) {
   const int64_t cells = (int64_t)B * X * Y * Z;
-  const K sentinel = (K)cells;  // above every valid key
-  const int nbits = std::max(1, bit_length((uint64_t)cells));
-  const int passes = (nbits + 7) / 8;
-  const int dbits_full = (nbits + passes - 1) / passes;
+  const int nbits = std::max(1, bit_length((uint64_t)(cells - 1)));
+  const int tb = std::min(nbits, TBMAX);
+  const int lb = nbits - tb;
+  const int nbk = 1 << tb;
   const int64_t ntiles = (N + RTILE - 1) / RTILE;
   const int64_t ncol = (int64_t)B * X * Y;
   const bool use_cols = ncol <= std::max<int64_t>(16 * N, int64_t(1) << 22);
-  const int64_t S = (int64_t)(1 << dbits_full) * ntiles;
+  const int64_t S = (int64_t)nbk * ntiles;
   size_t need = 2 * align_up((size_t)N * sizeof(K), 256) + 2 * align_up((size_t)N * 4, 256) +
-                align_up((size_t)S * 4, 256) + align_up(NBMAX * 4, 256) + (use_cols ? align_up((size_t)(ncol + 1) * 4, 256) : 0);
+                align_up((size_t)S * 4, 256) + align_up(NBMAX * 4, 256) +
+                align_up((size_t)ntiles * 4, 256) +
+                (use_cols ? align_up((size_t)(ncol + 1) * 4, 256) : 0);
   if (!keys_out) need += align_up((size_t)N * sizeof(K), 256);
   if (!perm_out) need += align_up((size_t)N * 4, 256);
   void* ws;
@@ -335,6 +736,7 @@ int radix_impl(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t B, int32_
   int32_t* vB = cv.take<int32_t>(N);
   int* counts = cv.take<int>(S);
   int* totals = cv.take<int>(NBMAX);
+  int* oob_tile = cv.take<int>(ntiles);
   int32_t* cols = use_cols ? cv.take<int32_t>(ncol + 1) : nullptr;
   K* kOut = keys_out ? (K*)keys_out : cv.take<K>(N);
   int32_t* vOut = perm_out ? perm_out : cv.take<int32_t>(N);
@@ -346,49 +748,40 @@ int radix_impl(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t B, int32_
   }
   {
     ProfScope p(ctx, "radix_pack");
-    pack_kernel<K><<<(unsigned)ntiles, RT, 0, s>>>((const int4*)coords, N, B, X, Y, Z, sentinel,
-                                                    kA, vA, 0, std::min(dbits_full, nbits),
-                                                    counts, (int)ntiles, status_dev);
+    pack_kernel<K><<<(unsigned)ntiles, RT, 0, s>>>((const int4*)coords, N, B, X, Y, Z,
+                                                    (K)(cells - 1), kA, vA, lb, tb, counts,
+                                                    (int)ntiles, oob_tile);
   }
-  K* kc = kA;
-  int32_t* vc = vA;
-  for (int p = 0; p < passes; ++p) {
-    const int shift = p * dbits_full;
-    const int dbits = std::min(dbits_full, nbits - shift);
-    K* kd = (p == passes - 1) ? kOut : (kc == kA ? kB : kA);
-    int32_t* vd = (p == passes - 1) ? vOut : (vc == vA ? vB : vA);
-    if (p > 0) {
-      ProfScope ps(ctx, "radix_hist");
-      hist_kernel<K><<<(unsigned)ntiles, RT, 0, s>>>(kc, N, shift, dbits, counts, (int)ntiles);
-    }
-    {
-      ProfScope ps(ctx, "radix_scan");
-      scan_kernel<<<(unsigned)(1 << dbits), RT, 0, s>>>(counts, (int)ntiles, totals);
-    }
-    {
-      ProfScope ps(ctx, "radix_scatter");
-      scatter_kernel<K><<<(unsigned)ntiles, RT, 0, s>>>(kc, vc, N, shift, dbits, counts, totals,
-                                                         (int)ntiles, kd, vd);
-    }
-    kc = kd;
-    vc = vd;
+  {
+    ProfScope ps(ctx, "radix_scan");
+    scan_kernel<<<(unsigned)nbk, RT, 0, s>>>(counts, (int)ntiles, totals, oob_tile, status_dev);
   }
-  if (use_cols) {
-    ProfScope ps(ctx, "radix_columns");
-    columns_kernel<K><<<(unsigned)((ncol + 1 + RT - 1) / RT), RT, 0, s>>>(kOut, N, Z, ncol, cols);
+  {
+    ProfScope ps(ctx, "radix_partition");
+    partition_kernel<K><<<(unsigned)ntiles, RT, 0, s>>>(kA, vA, N, lb, tb, counts, totals,
+                                                         (int)ntiles, kB, vB);
+  }
+  {
+    ProfScope ps(ctx, "radix_buckets");
+    bucket_sort_kernel<K><<<(unsigned)nbk, RT, 0, s>>>(kB, vB, kA, vA, kOut, vOut, totals, nbk,
+                                                        lb, cells, Z, ncol, N, cols);
   }
   {
     ProfScope ps(ctx, "radix_fill");
-    const int32_t per_xcd = mapk::fill_per_xcd(N);
-    const unsigned grid = (unsigned)per_xcd * 8u;
-    if (use_cols)
-      mapk::fill_columns_kernel<K, ColumnLookup<K, true>><<<grid, mapk::kFillThreads, 0, s>>>(
-          kOut, vOut, nullptr, N, sentinel, X, Y, Z, dil[0], dil[1], dil[2],
-          ColumnLookup<K, true>{kOut, cols, vOut, N}, per_xcd, nbr_out, status_dev);
-    else
+    const K no_sentinel = (K)-1;  // out-of-range voxels were clamped in pack
+    if (use_cols) {
+      const int64_t blocks = (N + kWinVox - 1) / kWinVox;
+      const int32_t per_xcd = (int32_t)((blocks + 7) / 8);
+      fill_window_kernel<K><<<(unsigned)per_xcd * 8u, kWinThreads, 0, s>>>(
+          kOut, vOut, cols, N, no_sentinel, mapk::KeyCoder<K>::make(X, Y, Z), dil[0], dil[1],
+          dil[2], ncol, per_xcd, nbr_out, status_dev);
+    } else {
+      const int32_t per_xcd = mapk::fill_per_xcd(N);
+      const unsigned grid = (unsigned)per_xcd * 8u;
       mapk::fill_columns_kernel<K, ColumnLookup<K, false>><<<grid, mapk::kFillThreads, 0, s>>>(
-          kOut, vOut, nullptr, N, sentinel, X, Y, Z, dil[0], dil[1], dil[2],
-          ColumnLookup<K, false>{kOut, nullptr, vOut, N}, per_xcd, nbr_out, status_dev);
+          kOut, vOut, nullptr, N, no_sentinel, mapk::KeyCoder<K>::make(X, Y, Z), dil[0], dil[1],
+          dil[2], ColumnLookup<K, false>{kOut, nullptr, vOut, N}, per_xcd, nbr_out, status_dev);
+    }
   }
   return check_hip(hipGetLastError(), "map_build_radix launch");
 }
