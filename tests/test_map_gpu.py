@@ -80,6 +80,34 @@ def test_map_edge_cases(pkg, dev, method):
     _check(m, big, 3, (1024, 1024, 700), (1, 1, 1))
 
 
+@pytest.mark.parametrize("method", METHODS)
+def test_map_dense_and_sparse_extremes(pkg, dev, method):
+    rng = np.random.default_rng(5)
+    # two dense 64x256 slabs in 256^3: key buckets of 16384 voxels (more than one sorting tile)
+    slab = np.array([[0, x, y, z] for x in (10, 11) for y in range(64) for z in range(256)], np.int32)
+    slab = np.concatenate([slab, np.array([[0, 200, 3, 4], [0, 12, 63, 255]], np.int32)])
+    slab = slab[rng.permutation(len(slab))]
+    m = _build(pkg, dev, slab, 1, (256, 256, 256), method=method)
+    _check(m, slab, 1, (256, 256, 256), (1, 1, 1))
+    # full columns of 100 voxels: long binary searches inside the fill windows
+    cols = np.array([[b, x, y, z] for b in range(2) for x in range(4) for y in range(5)
+                     for z in range(100)], np.int32)
+    cols = cols[rng.permutation(len(cols))]
+    m = _build(pkg, dev, cols, 2, (4, 5, 100), method=method)
+    _check(m, cols, 2, (4, 5, 100), (1, 1, 1))
+    # sparse random voxels in 512^3: consecutive sorted voxels far apart
+    flat = rng.choice(512 ** 3, size=20000, replace=False)
+    sparse = np.stack([np.zeros_like(flat), flat // (512 * 512), (flat // 512) % 512, flat % 512],
+                      axis=1).astype(np.int32)
+    m = _build(pkg, dev, sparse, 1, (512, 512, 512), method=method)
+    _check(m, sparse, 1, (512, 512, 512), (1, 1, 1))
+    # a repeated key inside a 2^18-cell grid is still reported after the bucket sort
+    dup = np.concatenate([cols[:500, 1:], cols[:1, 1:]])
+    dup = np.concatenate([np.zeros((len(dup), 1), np.int32), dup], axis=1)
+    with pytest.raises(pkg.TscError, match="duplicate"):
+        _build(pkg, dev, dup, 1, (64, 64, 64), method=method)
+
+
 def test_map_empty(pkg, dev):
     c = torch.zeros((0, 4), dtype=torch.int32, device=dev)
     m = pkg.build_neighbor_map(c, (4, 4, 4), 1)

@@ -19,6 +19,7 @@
 //              array when the column table would be much larger than the voxel set.
 
 #include <algorithm>
+#include <type_traits>
 
 #include "map_common.h"
 
@@ -31,10 +32,12 @@ constexpr int RTILE = RT * RI;      // elements per tile
 constexpr int WAVES = RT / 64;
 constexpr int TBMAX = 10;           // bucket digit bits
 constexpr int NBMAX = 1 << TBMAX;   // buckets
-constexpr int DPT = NBMAX / RT;     // bucket digits owned per thread in the partition prefix
 constexpr int LBITS = 9;            // local pass digit bits
 constexpr int LNB = 1 << LBITS;
 constexpr int LPT = LNB / RT;       // local digits owned per thread
+constexpr int PT = 512;             // pack / partition threads per block
+constexpr int PI = RTILE / PT;      // pack / partition items per thread
+constexpr int PDPT = NBMAX / PT;    // bucket digits owned per thread in the partition prefix
 
 template <typename K>
 __device__ __forceinline__ int digit_of(K k, int shift, int mask) {
@@ -46,20 +49,20 @@ __global__ void clear_status_kernel(uint32_t* status) {
 }
 
 template <typename K>
-__global__ void __launch_bounds__(RT)
+__global__ void __launch_bounds__(PT)
     pack_kernel(const int4* __restrict__ coords, int64_t N, int32_t B, int32_t X, int32_t Y,
                 int32_t Z, K last_cell, K* __restrict__ keys, int32_t* __restrict__ vals,
                 int shift, int dbits, int* __restrict__ counts, int ntiles,
                 int* __restrict__ oob_tile) {
   __shared__ int hist[NBMAX];
   const int nb = 1 << dbits, mask = nb - 1;
-  for (int d = threadIdx.x; d < nb; d += RT) hist[d] = 0;
+  for (int d = threadIdx.x; d < nb; d += PT) hist[d] = 0;
   __syncthreads();
   const int64_t base = (int64_t)blockIdx.x * RTILE;
   int oob = 0;
-#pragma unroll 4
-  for (int j = 0; j < RI; ++j) {
-    const int64_t e = base + j * RT + threadIdx.x;
+#pragma unroll
+  for (int j = 0; j < PI; ++j) {
+    const int64_t e = base + j * PT + threadIdx.x;
     if (e < N) {
       K key;
       if (!mapk::pack_key<K>(coords[e], B, X, Y, Z, &key)) {
@@ -72,7 +75,7 @@ __global__ void __launch_bounds__(RT)
     }
   }
   oob = __syncthreads_or(oob);
-  for (int d = threadIdx.x; d < nb; d += RT) counts[(int64_t)d * ntiles + blockIdx.x] = hist[d];
+  for (int d = threadIdx.x; d < nb; d += PT) counts[(int64_t)d * ntiles + blockIdx.x] = hist[d];
   if (threadIdx.x == 0) oob_tile[blockIdx.x] = oob;
 }
 
@@ -86,7 +89,8 @@ __device__ __forceinline__ int wave_incl_scan(int v) {
   return v;
 }
 
-// Exclusive scan of v over the block's threads; *total receives the block sum.
+// Exclusive scan of v over the block's NW waves; *total receives the block sum.
+template <int NW = WAVES>
 __device__ __forceinline__ int block_excl_scan(int v, int* wsum, int* total) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int incl = wave_incl_scan(v);
@@ -94,7 +98,7 @@ __device__ __forceinline__ int block_excl_scan(int v, int* wsum, int* total) {
   __syncthreads();
   int pre = incl - v, tot = 0;
 #pragma unroll
-  for (int ww = 0; ww < WAVES; ++ww) {
+  for (int ww = 0; ww < NW; ++ww) {
     if (ww < w) pre += wsum[ww];
     tot += wsum[ww];
   }
@@ -163,65 +167,66 @@ __device__ __forceinline__ void wave_rank(const K (&kk)[N_ITEMS], int64_t first,
 // LDS atomic.  The tile is reordered by digit in LDS and written as contiguous runs at
 // (all elements of smaller digits) + (this digit in earlier tiles).
 template <typename K>
-__global__ void __launch_bounds__(RT)
+__global__ void __launch_bounds__(PT)
     partition_kernel(const K* __restrict__ ksrc, const int32_t* __restrict__ vsrc, int64_t N,
                      int shift, int dbits, const int* __restrict__ offs,
                      const int* __restrict__ totals, int ntiles, K* __restrict__ kdst,
-                     int32_t* __restrict__ vdst) {
+                     int32_t* __restrict__ vdst, int* __restrict__ bstart) {
   __shared__ int lcnt[NBMAX];
   __shared__ int dstart[NBMAX];
   __shared__ int gbase[NBMAX];
-  __shared__ int wsum[WAVES];
+  __shared__ int wsum[PT / 64];
   __shared__ K sk[RTILE];
   __shared__ int32_t sv[RTILE];
   const int nb = 1 << dbits, mask = nb - 1;
   const int tid = threadIdx.x;
-  for (int i = tid; i < NBMAX; i += RT) lcnt[i] = 0;
+  for (int i = tid; i < NBMAX; i += PT) lcnt[i] = 0;
   __syncthreads();
   const int64_t tile0 = (int64_t)blockIdx.x * RTILE;
-  K kk[RI];
-  int32_t vv[RI];
-  int slot[RI];
+  K kk[PI];
+  int32_t vv[PI];
+  int slot[PI];
 #pragma unroll
-  for (int j = 0; j < RI; ++j) {
-    const int64_t e = tile0 + j * RT + tid;
+  for (int j = 0; j < PI; ++j) {
+    const int64_t e = tile0 + j * PT + tid;
     const bool valid = e < N;
     kk[j] = valid ? ksrc[e] : (K)0;
     vv[j] = valid ? vsrc[e] : 0;
   }
 #pragma unroll
-  for (int j = 0; j < RI; ++j) {
-    const int64_t e = tile0 + j * RT + tid;
+  for (int j = 0; j < PI; ++j) {
+    const int64_t e = tile0 + j * PT + tid;
     slot[j] = e < N ? atomicAdd(&lcnt[digit_of<K>(kk[j], shift, mask)], 1) : 0;
   }
   __syncthreads();
-  // Thread t owns digits [t*DPT, (t+1)*DPT): tile-local start of each digit and its global start.
-  int loc[DPT];
+  // Thread t owns digits [t*PDPT, (t+1)*PDPT): tile-local start of each digit and its global start.
+  int loc[PDPT];
   int tsum = 0, gsum = 0;
 #pragma unroll
-  for (int q = 0; q < DPT; ++q) {
-    const int d = tid * DPT + q;
+  for (int q = 0; q < PDPT; ++q) {
+    const int d = tid * PDPT + q;
     loc[q] = lcnt[d];
     tsum += loc[q];
     gsum += d < nb ? totals[d] : 0;
   }
   int dummy;
-  int pre = block_excl_scan(tsum, wsum, &dummy);
-  int gpre = block_excl_scan(gsum, wsum, &dummy);
+  int pre = block_excl_scan<PT / 64>(tsum, wsum, &dummy);
+  int gpre = block_excl_scan<PT / 64>(gsum, wsum, &dummy);
 #pragma unroll
-  for (int q = 0; q < DPT; ++q) {
-    const int d = tid * DPT + q;
+  for (int q = 0; q < PDPT; ++q) {
+    const int d = tid * PDPT + q;
     dstart[d] = pre;
     pre += loc[q];
     if (d < nb) {
       gbase[d] = gpre + offs[(int64_t)d * ntiles + blockIdx.x];
+      if (blockIdx.x == 0) bstart[d] = gpre;  // bucket start, for the bucket kernel
       gpre += totals[d];
     }
   }
   __syncthreads();
 #pragma unroll
-  for (int j = 0; j < RI; ++j) {
-    const int64_t e = tile0 + j * RT + tid;
+  for (int j = 0; j < PI; ++j) {
+    const int64_t e = tile0 + j * PT + tid;
     if (e < N) {
       const int p = dstart[digit_of<K>(kk[j], shift, mask)] + slot[j];
       sk[p] = kk[j];
@@ -231,7 +236,7 @@ __global__ void __launch_bounds__(RT)
   __syncthreads();
   const int64_t rem = N - tile0;
   const int tile_n = rem < RTILE ? (int)rem : RTILE;
-  for (int i = tid; i < tile_n; i += RT) {
+  for (int i = tid; i < tile_n; i += PT) {
     const K k = sk[i];
     const int d = digit_of<K>(k, shift, mask);
     const int64_t pos = (int64_t)gbase[d] + (i - dstart[d]);
@@ -289,76 +294,31 @@ __device__ __forceinline__ void wave_offsets(int (*wcnt)[LNB], int (&cnt)[LPT]) 
 
 // One block per bucket b (see the file comment).  The bucket occupies [start, start+size) of
 // (k0, v0) after the partition.
-//  * size <= RTILE and lb <= kBitmapBits (every int32-key grid up to 2^27 cells): the bucket is
-//    loaded into LDS once and each element sets bit (key mod 2^lb) of an LDS bitmap of the
-//    bucket's key range; with unique keys, an element's sorted position is the number of set
-//    bits below its own (per-word prefix counts + one popcount).  The sorted bucket is staged in
-//    LDS and stored with coalesced writes.
-//  * size <= RTILE otherwise, or when the bitmap finds a repeated key: stable LSD passes over the
-//    bucket's remaining bits in LDS (histogram of the pass digit, exclusive scan, wave_rank over
-//    wave-contiguous runs, scatter back into LDS), so equal keys end up adjacent for the fill's
-//    duplicate check.
-//  * larger buckets: the same LSD passes through global memory in chunks of RTILE, alternating
-//    between (k0, v0) and (k1, v1), the last pass writing (kout, vout).
-// Then col_start[c] for the columns whose first key c*Z lies in the bucket's key range.
+//  * size <= RTILE and lb <= kBitmapBits (every int32-key grid up to 2^27 cells): each thread
+//    loads its elements into registers and sets bit (key mod 2^lb) of an LDS bitmap of the
+//    bucket's key range.  With unique keys an element's sorted position is the number of set
+//    bits below its own (per-word prefix counts + one popcount), and so is every column start:
+//    col_start[c] = start + (set bits below c*Z - (b << lb)).
+//  * otherwise, or when the bitmap finds a repeated key: stable LSD passes over the bucket's
+//    remaining bits (at most 9 per pass) through global memory in chunks of RTILE (histogram of
+//    the pass digit, exclusive scan, wave_rank over wave-contiguous runs, scatter), alternating
+//    between (k0, v0) and (k1, v1), the last pass writing (kout, vout); equal keys end up
+//    adjacent for the fill's duplicate check.  Column starts then come from binary searches of
+//    the sorted bucket.
 constexpr int kBitmapBits = 17;
 constexpr int kBitmapWords = (1 << kBitmapBits) / 32;
 
 template <typename K>
-__device__ __forceinline__ void lsd_pass_lds(K* lk, int32_t* lv, int size, int shift, int dbits,
-                                             int* run, int (*wcnt)[LNB], int* wsum) {
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int mask = (1 << dbits) - 1;
-  // Wave w ranks elements [w*ipw*64, (w+1)*ipw*64): ipw rows of 64 per wave.
-  const int ipw = ((size + 63) / 64 + WAVES - 1) / WAVES;
-  const int wfirst = w * ipw * 64;
-  const int wlimit = min(size, wfirst + ipw * 64);
-  for (int d = tid; d < LNB; d += RT) run[d] = 0;
-  for (int i = tid; i < WAVES * LNB; i += RT) (&wcnt[0][0])[i] = 0;
-  __syncthreads();
-  for (int i = tid; i < size; i += RT) atomicAdd(&run[digit_of<K>(lk[i], shift, mask)], 1);
-  K kk[RI];
-  int32_t vv[RI];
-  int lr[RI];
-#pragma unroll
-  for (int j = 0; j < RI; ++j) {
-    const int e = wfirst + j * 64 + lane;
-    const bool valid = e < wlimit;
-    kk[j] = valid ? lk[e] : (K)0;
-    vv[j] = valid ? lv[e] : 0;
-  }
-  __syncthreads();
-  scan_bins(run, wsum);
-  wave_rank<K, RI>(kk, wfirst, wlimit, shift, dbits, wcnt[w], lr);
-  __syncthreads();
-  int cnt[LPT];
-  wave_offsets(wcnt, cnt);
-  __syncthreads();
-#pragma unroll
-  for (int j = 0; j < RI; ++j) {
-    const int e = wfirst + j * 64 + lane;
-    if (e < wlimit) {
-      const int d = digit_of<K>(kk[j], shift, mask);
-      const int pos = run[d] + wcnt[w][d] + lr[j];
-      lk[pos] = kk[j];
-      lv[pos] = vv[j];
-    }
-  }
-  __syncthreads();
-}
-
-template <typename K>
 __global__ void __launch_bounds__(RT)
     bucket_sort_kernel(K* k0, int32_t* v0, K* k1, int32_t* v1, K* __restrict__ kout,
-                       int32_t* __restrict__ vout, const int* __restrict__ totals, int nbk,
+                       int32_t* __restrict__ vout, const int* __restrict__ totals,
+                       const int* __restrict__ bstart, int nbk,
                        int lb, int64_t cells, int64_t Z, int64_t ncol, int64_t n,
                        int32_t* __restrict__ col_start) {
-  // smem: the key bitmap, or (after it) the LSD digit counters run[LNB] + wcnt[WAVES][LNB].
+  // smem: the key bitmap, or the LSD digit counters run[LNB] + wcnt[WAVES][LNB].
   __shared__ uint32_t smem[kBitmapWords];
   __shared__ uint16_t wpre[kBitmapWords];  // set bits in the words before each word
   __shared__ int wsum[WAVES];
-  __shared__ K lk[RTILE];
-  __shared__ int32_t lv[RTILE];
   static_assert(kBitmapWords >= LNB * (WAVES + 1), "LSD counters alias the bitmap");
   static_assert(RTILE <= 65535, "prefix counts fit 16 bits");
   uint32_t* bits = smem;
@@ -366,87 +326,72 @@ __global__ void __launch_bounds__(RT)
   int(*wcnt)[LNB] = (int(*)[LNB])((int*)smem + LNB);
   const int tid = threadIdx.x;
   const int b = blockIdx.x;
-  int part = 0;
-  for (int d = tid; d < b; d += RT) part += totals[d];
-  int start32;
-  (void)block_excl_scan(part, wsum, &start32);
-  const int64_t start = start32;
+  const int64_t start = bstart[b];
   const int size = totals[b];
-  const bool fits = size <= RTILE;
   const int passes = (lb + LBITS - 1) / LBITS;
   const int pbits = passes ? (lb + passes - 1) / passes : 0;
+  const K lmask = (K)(((uint64_t)1 << lb) - 1);
 
-  if (fits) {
-    for (int i = tid; i < size; i += RT) {
-      lk[i] = k0[start + i];
-      lv[i] = v0[start + i];
+  bool by_bitmap = false;
+  if (size <= RTILE && lb <= kBitmapBits && passes > 0) {
+    const int nwords = ((1 << lb) + 31) / 32;
+    for (int i = tid; i < nwords; i += RT) bits[i] = 0u;
+    __syncthreads();
+    K kk[RI];
+    int32_t vv[RI];
+    int loc[RI];
+    int dup = 0;
+#pragma unroll
+    for (int j = 0; j < RI; ++j) {
+      const int i = j * RT + tid;
+      if (i < size) {
+        kk[j] = k0[start + i];
+        vv[j] = v0[start + i];
+      }
     }
-    bool sorted = passes == 0;
-    if (!sorted && lb <= kBitmapBits) {
-      const int nwords = ((1 << lb) + 31) / 32;
-      const K lmask = (K)((1u << lb) - 1u);
-      for (int i = tid; i < nwords; i += RT) bits[i] = 0u;
+#pragma unroll
+    for (int j = 0; j < RI; ++j) {
+      const int i = j * RT + tid;
+      if (i < size) {
+        loc[j] = (int)(kk[j] & lmask);
+        const uint32_t bit = 1u << (loc[j] & 31);
+        dup |= (atomicOr(&bits[loc[j] >> 5], bit) & bit) != 0u;
+      }
+    }
+    dup = __syncthreads_or(dup);
+    if (!dup) {
+      // Per-word prefix counts: thread t owns words [t*wpt, (t+1)*wpt).
+      const int wpt = (nwords + RT - 1) / RT;
+      int sum = 0;
+      for (int q = 0; q < wpt; ++q) {
+        const int wi = tid * wpt + q;
+        if (wi < nwords) sum += __popc(bits[wi]);
+      }
+      int tot;
+      int pre = block_excl_scan(sum, wsum, &tot);
+      for (int q = 0; q < wpt; ++q) {
+        const int wi = tid * wpt + q;
+        if (wi < nwords) {
+          wpre[wi] = (uint16_t)pre;
+          pre += __popc(bits[wi]);
+        }
+      }
       __syncthreads();
-      K kk[RI];
-      int32_t vv[RI];
-      int loc[RI];
-      int dup = 0;
 #pragma unroll
       for (int j = 0; j < RI; ++j) {
         const int i = j * RT + tid;
         if (i < size) {
-          kk[j] = lk[i];
-          vv[j] = lv[i];
-          loc[j] = (int)(kk[j] & lmask);
-          const uint32_t bit = 1u << (loc[j] & 31);
-          dup |= (atomicOr(&bits[loc[j] >> 5], bit) & bit) != 0u;
+          const int wi = loc[j] >> 5;
+          const int r = wpre[wi] + __popc(bits[wi] & ((1u << (loc[j] & 31)) - 1u));
+          kout[start + r] = kk[j];
+          vout[start + r] = vv[j];
         }
       }
-      dup = __syncthreads_or(dup);
-      if (!dup) {
-        // Per-word prefix counts: thread t owns words [t*wpt, (t+1)*wpt).
-        const int wpt = (nwords + RT - 1) / RT;
-        int sum = 0;
-        for (int q = 0; q < wpt; ++q) {
-          const int wi = tid * wpt + q;
-          if (wi < nwords) sum += __popc(bits[wi]);
-        }
-        int tot;
-        int pre = block_excl_scan(sum, wsum, &tot);
-        for (int q = 0; q < wpt; ++q) {
-          const int wi = tid * wpt + q;
-          if (wi < nwords) {
-            wpre[wi] = (uint16_t)pre;
-            pre += __popc(bits[wi]);
-          }
-        }
-        __syncthreads();
-#pragma unroll
-        for (int j = 0; j < RI; ++j) {
-          const int i = j * RT + tid;
-          if (i < size) {
-            const int wi = loc[j] >> 5;
-            const int r = wpre[wi] + __popc(bits[wi] & ((1u << (loc[j] & 31)) - 1u));
-            lk[r] = kk[j];
-            lv[r] = vv[j];
-          }
-        }
-        sorted = true;
-      }
-      __syncthreads();
+      by_bitmap = true;
     }
-    if (!sorted) {
-      for (int p = 0; p < passes; ++p) {
-        const int shift = p * pbits;
-        lsd_pass_lds<K>(lk, lv, size, shift, min(pbits, lb - shift), run, wcnt, wsum);
-      }
-    }
-    __syncthreads();
-    for (int i = tid; i < size; i += RT) {
-      kout[start + i] = lk[i];
-      vout[start + i] = lv[i];
-    }
-  } else {
+  }
+  if (!by_bitmap) {
+    const int lane = tid & 63, w = tid >> 6;
     for (int p = 0; p < passes; ++p) {
       const int shift = p * pbits;
       const int dbits = min(pbits, lb - shift);
@@ -456,7 +401,7 @@ __global__ void __launch_bounds__(RT)
       const int32_t* vs = (p & 1) ? v1 : v0;
       K* kd = last ? kout : ((p & 1) ? k0 : k1);
       int32_t* vd = last ? vout : ((p & 1) ? v0 : v1);
-      const int lane = tid & 63, w = tid >> 6;
+      __syncthreads();
       for (int d = tid; d < LNB; d += RT) run[d] = 0;
       __syncthreads();
       for (int i = tid; i < size; i += RT)
@@ -513,18 +458,13 @@ __global__ void __launch_bounds__(RT)
   const int64_t key_hi = std::min<int64_t>((int64_t)(b + 1) << lb, cells);
   const int64_t c_lo = (key_lo + Z - 1) / Z, c_hi = (key_hi + Z - 1) / Z;
   for (int64_t c = c_lo + tid; c < c_hi; c += RT) {
-    const K t = (K)(c * Z);
     int64_t pos;
-    if (fits) {
-      int lo = 0, hi = size;
-      while (lo < hi) {
-        const int mid = (lo + hi) >> 1;
-        if (lk[mid] < t) lo = mid + 1;
-        else hi = mid;
-      }
-      pos = lo;
+    if (by_bitmap) {
+      const int local = (int)(c * Z - key_lo);
+      const int wi = local >> 5;
+      pos = wpre[wi] + __popc(bits[wi] & ((1u << (local & 31)) - 1u));
     } else {
-      pos = lower_bound<K>(kout + start, 0, size, t);
+      pos = lower_bound<K>(kout + start, 0, size, (K)(c * Z));
     }
     col_start[c] = (int32_t)(start + pos);
   }
@@ -564,52 +504,71 @@ struct ColumnLookup {
 // Window fill: a block owns kWinVox consecutive sorted voxels.  Their columns span
 // [c_first, c_last]; every neighbor column with offset (kd-1)*dD along x lies in
 // [c_first + (kd-1)*dD*Y - dH, c_last + (kd-1)*dD*Y + dH], and the sorted voxels of those
-// columns are one contiguous run of the sorted arrays.  Phase 1 copies, per kd, that run's z
-// values and rows plus the column starts into LDS with coalesced loads; phase 2 resolves every
-// probe from LDS (9 lanes per voxel as in the column-parallel fill), so the only global traffic
-// left per probe is the 12-byte row write.  A kd window that does not fit (very sparse or very
-// dense regions) falls back to the global column lookup for that kd only.
+// columns are one contiguous run of the sorted arrays.  Phase 1 decodes the block's voxels once
+// (column, z, row, a 9-bit mask of in-grid neighbor columns, the duplicate check) and copies,
+// per kd, that run's z values and rows plus the column starts into LDS with coalesced loads.
+// Phase 2 resolves every probe from LDS with 9 lanes per voxel (one per neighbor column, as in
+// the column-parallel fill): a binary search for the first z >= z - dW in the column, then at
+// most 2*dW + 1 consecutive entries.  A kd window that does not fit (very sparse or very dense
+// regions) falls back to the global column lookup for that kd only.
 constexpr int kWinThreads = 256;
 constexpr int kWinRounds = 8;
 constexpr int kWinVox = kWinRounds * mapk::kFillVoxPerWave * (kWinThreads / 64);  // 224
-constexpr int kWinCapE = 512;  // voxels per kd window
-constexpr int kWinCapC = 512;  // columns per kd window (LDS ~20 KB per block: 8 blocks per CU)
+constexpr int kWinCapE = 464;  // voxels per kd window
+constexpr int kWinCapC = 432;  // columns per kd window (LDS < 20 KB per block: 8 blocks per CU)
 
 template <typename K>
 __global__ void __launch_bounds__(kWinThreads)
     fill_window_kernel(const K* __restrict__ keys, const int32_t* __restrict__ perm,
-                       const int32_t* __restrict__ col_start, int64_t n, K sentinel,
-                       mapk::KeyCoder<K> kc_, int32_t dD, int32_t dH, int32_t dW, int64_t ncol,
-                       int32_t per_xcd, int32_t* __restrict__ nbr, uint32_t* __restrict__ status) {
-  __shared__ int32_t lz[3][kWinCapE];
-  __shared__ int32_t lp[3][kWinCapE];
+                       const int32_t* __restrict__ col_start, int64_t n, mapk::KeyCoder<K> kc_,
+                       int32_t dD, int32_t dH, int32_t dW, int64_t ncol, int32_t per_xcd,
+                       int32_t* __restrict__ nbr, uint32_t* __restrict__ status) {
+  using I = typename std::conditional<sizeof(K) == 4, int32_t, int64_t>::type;  // column index
+  __shared__ int32_t lz[3][kWinCapE + 4];  // +4: the probe reads up to 2 past a column's end
+  __shared__ int32_t lp[3][kWinCapE + 4];
   __shared__ int32_t lcs[3][kWinCapC + 1];
-  __shared__ int64_t w_lo[3];
+  __shared__ I w_lo[3];
   __shared__ int32_t w_e0[3], w_ne[3], w_nc[3];
-  __shared__ int64_t c_range[2];
-  __shared__ K sk[kWinVox + 1];  // sk[0] = key before the block (duplicate check)
-  __shared__ int32_t sp[kWinVox];
+  __shared__ I c_range[2];
+  __shared__ int32_t w_maxlen;  // longest column in the three windows
+  __shared__ I vcol[kWinVox];
+  __shared__ int32_t vz[kWinVox], vrow[kWinVox], vmask[kWinVox];
   const int tid = threadIdx.x;
   const int32_t X = kc_.X, Y = kc_.Y, Z = kc_.Z;
   const int64_t logical = (int64_t)(blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
   const int64_t i0 = logical * kWinVox;
   if (i0 >= n) return;  // uniform per block
-  const int64_t i1 = (i0 + kWinVox < n) ? i0 + kWinVox : n;
-  const int nv = (int)(i1 - i0);
-  if (tid < 2) {
-    const K k = keys[tid == 0 ? i0 : i1 - 1];
-    const int64_t c = (int64_t)kc_.column_of(k);
-    c_range[tid] = c < ncol ? c : ncol - 1;  // the sentinel key maps past the last column
+  const int nv = (int)((i0 + kWinVox < n) ? kWinVox : n - i0);
+  int dup = 0;
+  for (int j = tid; j < nv; j += kWinThreads) {
+    const K key = keys[i0 + j];
+    K column;
+    int32_t x, y, z;
+    kc_.decode(key, &column, &x, &y, &z);
+    int m = 0;
+#pragma unroll
+    for (int kd = 0; kd < 3; ++kd) {
+#pragma unroll
+      for (int kh = 0; kh < 3; ++kh) {
+        const bool in = (uint32_t)(x + (kd - 1) * dD) < (uint32_t)X &&
+                        (uint32_t)(y + (kh - 1) * dH) < (uint32_t)Y;
+        m |= (int)in << (kd * 3 + kh);
+      }
+    }
+    vcol[j] = (I)column;
+    vz[j] = z;
+    vmask[j] = m;
+    vrow[j] = perm[i0 + j];
+    if (i0 + j > 0 && keys[i0 + j - 1] == key) dup = 1;
+    if (j == 0) c_range[0] = (I)column;
+    if (j == nv - 1) c_range[1] = (I)column;
   }
-  for (int j = tid; j <= nv; j += kWinThreads) {
-    const int64_t e = i0 - 1 + j;
-    sk[j] = e >= 0 ? keys[e] : (K)-1;
-    if (j > 0) sp[j - 1] = perm[e];
-  }
-  __syncthreads();
+  if (tid == 0) w_maxlen = 0;
+  dup = __syncthreads_or(dup);
+  if (dup && tid == 0) atomicOr(status, TSC_MAP_DUPLICATE);
   if (tid < 3) {
     const int64_t shiftc = (int64_t)(tid - 1) * dD * Y;
-    int64_t lo = c_range[0] + shiftc - dH, hi = c_range[1] + shiftc + dH;
+    int64_t lo = (int64_t)c_range[0] + shiftc - dH, hi = (int64_t)c_range[1] + shiftc + dH;
     if (lo < 0) lo = 0;
     if (hi > ncol - 1) hi = ncol - 1;
     int32_t e0 = 0, ne = 0, nc = 0;
@@ -621,7 +580,7 @@ __global__ void __launch_bounds__(kWinThreads)
     } else if (lo <= hi) {
       nc = -1;
     }
-    w_lo[tid] = lo;
+    w_lo[tid] = (I)lo;
     w_e0[tid] = e0;
     w_ne[tid] = ne;
     w_nc[tid] = nc;  // -1: window does not fit, probes of this kd go to global memory
@@ -631,7 +590,7 @@ __global__ void __launch_bounds__(kWinThreads)
   for (int w = 0; w < 3; ++w) {
     const int nc = w_nc[w];
     if (nc <= 0) continue;
-    const int64_t lo = w_lo[w];
+    const I lo = w_lo[w];
     const int32_t e0 = w_e0[w], ne = w_ne[w];
     for (int j = tid; j <= nc; j += kWinThreads) lcs[w][j] = col_start[lo + j] - e0;
     for (int j = tid; j < ne; j += kWinThreads) {
@@ -641,60 +600,125 @@ __global__ void __launch_bounds__(kWinThreads)
   }
   __syncthreads();
 
+  {
+    int mx = 0;
+#pragma unroll
+    for (int w = 0; w < 3; ++w) {
+      const int nc = w_nc[w];
+      for (int j = tid; j < nc; j += kWinThreads) mx = max(mx, lcs[w][j + 1] - lcs[w][j]);
+    }
+    if (mx > 0) atomicMax(&w_maxlen, mx);
+  }
+  __syncthreads();
+
   const int lane = tid & 63, wid = tid >> 6;
   const int slot = lane / mapk::kFillLanes, col = lane - slot * mapk::kFillLanes;
   if (slot >= mapk::kFillVoxPerWave) return;
   const int kd = col / 3, kh = col - kd * 3;
   const int nc_w = w_nc[kd];
-  const int64_t lo_w = w_lo[kd];
-  ColumnLookup<K, true> glk{keys, col_start, perm, n};
-  for (int r = 0; r < kWinRounds; ++r) {
-    const int li = (wid * kWinRounds + r) * mapk::kFillVoxPerWave + slot;
-    if (li >= nv) break;
-    const K key = sk[li + 1];
-    if (key == sentinel) {  // out-of-range voxel: reported, no row written
-      if (col == 0) atomicOr(status, TSC_MAP_OUT_OF_RANGE);
-      continue;
-    }
-    if (col == 0 && sk[li] == key) atomicOr(status, TSC_MAP_DUPLICATE);
-    const int32_t row = sp[li];
-    K column;
-    int32_t x, y, z;
-    kc_.decode(key, &column, &x, &y, &z);
-    const int32_t nx = x + (kd - 1) * dD, ny = y + (kh - 1) * dH;
-    int32_t v[3] = {-1, -1, -1};
-    if ((uint32_t)nx < (uint32_t)X && (uint32_t)ny < (uint32_t)Y) {
-      const int64_t ncl = (int64_t)column + (int64_t)(kd - 1) * dD * Y + (kh - 1) * dH;
-      if (nc_w > 0) {
-        const int j = (int)(ncl - lo_w);
-        int a = lcs[kd][j];
-        const int e = lcs[kd][j + 1];
-        const bool has_lo = z - dW >= 0, has_hi = z + dW < Z;
-        const int32_t first = has_lo ? z - dW : z, last = has_hi ? z + dW : z;
-        int b = e;
-        while (a < b) {  // first entry with z >= first
-          const int mid = (a + b) >> 1;
-          if (lz[kd][mid] < first) a = mid + 1;
-          else b = mid;
-        }
-        for (; a < e; ++a) {
-          const int32_t zz = lz[kd][a];
-          if (zz > last) break;
-          if (zz == z) v[1] = lp[kd][a];
-          else if (has_lo && zz == z - dW) v[0] = lp[kd][a];
-          else if (has_hi && zz == z + dW) v[2] = lp[kd][a];
-        }
-      } else {
-        const K kc = (K)((int64_t)key + (int64_t)((kd - 1) * dD) * ((int64_t)Y * Z) +
-                         (int64_t)((kh - 1) * dH) * Z);
-        glk.column(kc, (K)ncl, z, Z, dW, v);
+  const I lo_w = w_lo[kd];
+  const I off = (I)(kd - 1) * dD * Y + (I)(kh - 1) * dH;
+  const int32_t* const wz = lz[kd];
+  const int32_t* const wp = lp[kd];
+  const int32_t* const wc = lcs[kd];
+  const int li0 = wid * kWinRounds * mapk::kFillVoxPerWave + slot;
+  if (dW == 1 && w_nc[0] >= 0 && w_nc[1] >= 0 && w_nc[2] >= 0) {
+    // Every window fits (block-uniform): branch-free probes.  A column's first entry with
+    // z >= z-1 comes from a binary search with a block-uniform step count (powers of two below
+    // the longest column); the taps z-1, z, z+1 can only be that entry and the next two.
+    int steps = 0;
+    while ((2 << steps) <= w_maxlen) ++steps;  // 2^steps <= maxlen < 2^(steps+1)
+    const int top = w_maxlen > 0 ? 1 << steps : 0;
+    const int jmax = nc_w > 0 ? nc_w - 1 : 0;
+#pragma unroll
+    for (int r = 0; r < kWinRounds; ++r) {
+      const int li = li0 + r * mapk::kFillVoxPerWave;
+      const bool live = li < nv;
+      const int lic = live ? li : 0;
+      const int32_t row = vrow[lic];
+      const int32_t z = vz[lic];
+      const bool inb = ((vmask[lic] >> col) & 1) && live;
+      int j = (int)(vcol[lic] + off - lo_w);
+      j = j < 0 ? 0 : (j > jmax ? jmax : j);
+      const int a = nc_w > 0 ? wc[j] : 0;  // an empty window (nc_w == 0) has no in-grid column
+      const int e = (inb && nc_w > 0) ? wc[j + 1] : a;
+      const int32_t first = z > 0 ? z - 1 : z;
+      int pos = a;
+      for (int st = top; st > 0; st >>= 1) {  // uniform trip count, no lane branches
+        const int t = pos + st;
+        int idx = (t < e ? t : e) - 1;
+        idx = idx < 0 ? 0 : idx;
+        const int32_t zv = wz[idx];
+        pos = ((t <= e) & (zv < first)) ? t : pos;
+      }
+      // pos <= e <= kWinCapE, so pos + 2 stays inside the padded arrays.
+      const int32_t z0 = wz[pos], z1 = wz[pos + 1], z2 = wz[pos + 2];
+      const int32_t p0 = wp[pos], p1 = wp[pos + 1], p2 = wp[pos + 2];
+      const bool ok0 = pos < e, ok1 = pos + 1 < e, ok2 = pos + 2 < e;
+      const int32_t zm = z > 0 ? z - 1 : -2, zp = z + 1 < Z ? z + 1 : -2;
+      // Entries from pos on are >= z-1 (>= z when z == 0) and strictly increasing, so z-1 can
+      // only sit at pos, z at pos or pos+1, z+1 at pos, pos+1 or pos+2.
+      const int32_t v0 = (ok0 & (z0 == zm)) ? p0 : -1;
+      int32_t v1 = (ok0 & (z0 == z)) ? p0 : -1;
+      v1 = (ok1 & (z1 == z)) ? p1 : v1;
+      int32_t v2 = (ok0 & (z0 == zp)) ? p0 : -1;
+      v2 = (ok1 & (z1 == zp)) ? p1 : v2;
+      v2 = (ok2 & (z2 == zp)) ? p2 : v2;
+      if (col == 4) v1 = row;  // tap 13 is the voxel itself
+      if (live) {
+        int32_t* dst = nbr + (int64_t)row * 27 + col * 3;
+        dst[0] = v0;
+        dst[1] = v1;
+        dst[2] = v2;
       }
     }
-    if (col == 4) v[1] = row;  // tap 13 is the voxel itself
+    return;
+  }
+  const int nscan = 2 * dW + 1;
+  ColumnLookup<K, true> glk{keys, col_start, perm, n};
+  for (int r = 0; r < kWinRounds; ++r) {
+    const int li = li0 + r * mapk::kFillVoxPerWave;
+    if (li >= nv) break;
+    const int32_t row = vrow[li];
+    int32_t v0 = -1, v1 = -1, v2 = -1;
+    if ((vmask[li] >> col) & 1) {
+      const I ncl = vcol[li] + off;
+      const int32_t z = vz[li];
+      const bool has_lo = z - dW >= 0, has_hi = z + dW < Z;
+      if (nc_w > 0) {
+        const int j = (int)(ncl - lo_w);
+        int a = wc[j];
+        int b = wc[j + 1];
+        const int e = b;
+        const int32_t first = has_lo ? z - dW : z;
+        while (a < b) {  // first entry with z >= first
+          const int mid = (a + b) >> 1;
+          if (wz[mid] < first) a = mid + 1;
+          else b = mid;
+        }
+        const int32_t last = has_hi ? z + dW : z;
+        for (int t = 0; t < nscan; ++t, ++a) {
+          if (a >= e) break;
+          const int32_t zz = wz[a];
+          if (zz > last) break;
+          const int32_t p = wp[a];
+          if (zz == z) v1 = p;
+          else if (has_lo && zz == z - dW) v0 = p;
+          else if (has_hi && zz == z + dW) v2 = p;
+        }
+      } else {
+        int32_t v[3] = {-1, -1, -1};
+        glk.column((K)((K)ncl * Z + z), (K)ncl, z, Z, dW, v);
+        v0 = v[0];
+        v1 = v[1];
+        v2 = v[2];
+      }
+    }
+    if (col == 4) v1 = row;  // tap 13 is the voxel itself
     int32_t* dst = nbr + (int64_t)row * 27 + col * 3;
-    dst[0] = v[0];
-    dst[1] = v[1];
-    dst[2] = v[2];
+    dst[0] = v0;
+    dst[1] = v1;
+    dst[2] = v2;
   }
 }
 
@@ -722,7 +746,7 @@ int radix_impl(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t B, int32_
   const int64_t S = (int64_t)nbk * ntiles;
   size_t need = 2 * align_up((size_t)N * sizeof(K), 256) + 2 * align_up((size_t)N * 4, 256) +
                 align_up((size_t)S * 4, 256) + align_up(NBMAX * 4, 256) +
-                align_up((size_t)ntiles * 4, 256) +
+                align_up((size_t)ntiles * 4, 256) + align_up(NBMAX * 4, 256) +
                 (use_cols ? align_up((size_t)(ncol + 1) * 4, 256) : 0);
   if (!keys_out) need += align_up((size_t)N * sizeof(K), 256);
   if (!perm_out) need += align_up((size_t)N * 4, 256);
@@ -737,6 +761,7 @@ int radix_impl(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t B, int32_
   int* counts = cv.take<int>(S);
   int* totals = cv.take<int>(NBMAX);
   int* oob_tile = cv.take<int>(ntiles);
+  int* bstart = cv.take<int>(NBMAX);
   int32_t* cols = use_cols ? cv.take<int32_t>(ncol + 1) : nullptr;
   K* kOut = keys_out ? (K*)keys_out : cv.take<K>(N);
   int32_t* vOut = perm_out ? perm_out : cv.take<int32_t>(N);
@@ -748,7 +773,7 @@ int radix_impl(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t B, int32_
   }
   {
     ProfScope p(ctx, "radix_pack");
-    pack_kernel<K><<<(unsigned)ntiles, RT, 0, s>>>((const int4*)coords, N, B, X, Y, Z,
+    pack_kernel<K><<<(unsigned)ntiles, PT, 0, s>>>((const int4*)coords, N, B, X, Y, Z,
                                                     (K)(cells - 1), kA, vA, lb, tb, counts,
                                                     (int)ntiles, oob_tile);
   }
@@ -758,12 +783,13 @@ int radix_impl(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t B, int32_
   }
   {
     ProfScope ps(ctx, "radix_partition");
-    partition_kernel<K><<<(unsigned)ntiles, RT, 0, s>>>(kA, vA, N, lb, tb, counts, totals,
-                                                         (int)ntiles, kB, vB);
+    partition_kernel<K><<<(unsigned)ntiles, PT, 0, s>>>(kA, vA, N, lb, tb, counts, totals,
+                                                         (int)ntiles, kB, vB, bstart);
   }
   {
     ProfScope ps(ctx, "radix_buckets");
-    bucket_sort_kernel<K><<<(unsigned)nbk, RT, 0, s>>>(kB, vB, kA, vA, kOut, vOut, totals, nbk,
+    bucket_sort_kernel<K><<<(unsigned)nbk, RT, 0, s>>>(kB, vB, kA, vA, kOut, vOut, totals,
+                                                        bstart, nbk,
                                                         lb, cells, Z, ncol, N, cols);
   }
   {
@@ -773,8 +799,8 @@ int radix_impl(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t B, int32_
       const int64_t blocks = (N + kWinVox - 1) / kWinVox;
       const int32_t per_xcd = (int32_t)((blocks + 7) / 8);
       fill_window_kernel<K><<<(unsigned)per_xcd * 8u, kWinThreads, 0, s>>>(
-          kOut, vOut, cols, N, no_sentinel, mapk::KeyCoder<K>::make(X, Y, Z), dil[0], dil[1],
-          dil[2], ncol, per_xcd, nbr_out, status_dev);
+          kOut, vOut, cols, N, mapk::KeyCoder<K>::make(X, Y, Z), dil[0], dil[1], dil[2], ncol,
+          per_xcd, nbr_out, status_dev);
     } else {
       const int32_t per_xcd = mapk::fill_per_xcd(N);
       const unsigned grid = (unsigned)per_xcd * 8u;
