@@ -37,7 +37,13 @@ PEAK_HBM = 8.0e12          # B/s, MI355X HBM3E
 PEAK_MFMA = {"bfloat16": 2.5e15, "float16": 2.5e15, "float32": 157.3e12}  # dense FLOP/s
 MAP_BYTES_PER_VOXEL = 128  # 16 coords + 4 key + 108 table
 # Algorithmic bytes per voxel of each map-build kernel (inputs it must read + outputs it writes).
-MAP_KERNEL_BYTES = {"map_mark": 16, "map_place": 16 + 4 + 4, "map_fill": 4 + 4 + 108}
+MAP_KERNEL_BYTES = {
+    "map_mark": 16, "map_place": 16 + 4 + 4, "map_fill": 4 + 4 + 108,   # bitmap path
+    "radix_pack": 16 + 4 + 4,          # coords in; (key, row) out
+    "radix_partition": 8 + 8,          # (key, row) in and out
+    "radix_buckets": 8 + 8,            # (key, row) in; sorted key + row out (column table extra)
+    "radix_fill": 4 + 4 + 108,         # sorted key + row in; 27 neighbor rows out
+}
 
 
 def log(msg: str) -> None:
@@ -77,9 +83,11 @@ def kernel_times(ctx, fn, steps: int) -> dict:
 
 # Library profiler names -> the kernel names profiles/traffic.json uses (rocprofv3 symbols
 # shortened by trellis.2-stableprojectorz_amd/profiling.py).
-ROCPROF_NAME = {"map_fill": "fill_columns_kernel<bitmap>", "radix_fill": "fill_columns_kernel<radix>",
-                "map_mark": "mark_kernel<int32>", "map_place": "place_kernel<int32>",
-                "radix_scatter": "scatter_kernel<int32>", "radix_pack": "pack_kernel<int32>"}
+ROCPROF_NAME = {"map_fill": "fill_columns_kernel<bitmap>", "map_mark": "mark_kernel<int32>",
+                "map_place": "place_kernel<int32>", "radix_fill": "fill_window_kernel<int32>",
+                "radix_buckets": "bucket_sort_kernel<int32>",
+                "radix_partition": "partition_kernel<int32>", "radix_pack": "pack_kernel<int32>",
+                "radix_scan": "scan_kernel"}
 
 
 def load_traffic(kernel: str):

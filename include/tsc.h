@@ -102,11 +102,22 @@ int tsc_map_build(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t B, int
                   int32_t Z, const int32_t kernel[3], const int32_t dilation[3], int32_t method,
                   void* keys_out, int32_t* perm_out, int32_t* nbr_out, uint32_t* status_dev);
 
+/* Row order for tsc_conv / tsc_conv_fused / tsc_resblock: the map's sorted rows (perm, from
+ * tsc_map_build; NULL = 0..N-1) regrouped inside windows of 16384 consecutive entries so that rows
+ * with the same set of present neighbors are contiguous.  The conv kernels skip a tap for a tile
+ * of rows only when no row of the tile has that neighbor, so grouped rows skip far more absent
+ * (zero) neighbor work than key order does on thin shells.  order_out: device int32 (N).
+ * No counterpart in the reference: an acceleration structure derived from the neighbor map,
+ * meant to be cached beside it (the reference caches the map per tensor, conv3d.ts:144-148). */
+int tsc_map_conv_order(tsc_ctx* ctx, const int32_t* nbr, const int32_t* perm, int64_t N,
+                       int32_t* order_out);
+
 /* ---- convolution -------------------------------------------------------------------------- */
 /* out[n,co] = bias[co] + sum_{v: nbr[n,v]>=0} sum_ci feats[nbr[n,v],ci] * W[co,v,ci]
  *   feats (N,Ci), weight (Co,3,3,3,Ci), bias (Co) or NULL, out (N,Co): all `dtype`, row-major.
- *   order: optional device int32 (N) permutation; rows are processed in that order (pass the
- *   map's perm_out for spatial locality).  NULL = 0..N-1.  Results do not depend on it.
+ *   order: optional device int32 (N) permutation; rows are processed in that order (pass
+ *   tsc_map_conv_order's output, or the map's perm_out for spatial locality).  NULL = 0..N-1.
+ *   Results do not depend on it.
  * Replaces conv3d.ts:154-221 / conv3d_wgsl.ts:132-231.  Ci and Co must be multiples of 16. */
 int tsc_conv(tsc_ctx* ctx, int32_t dtype, const void* feats, const void* weight, const void* bias,
              const int32_t* nbr, const int32_t* order, int64_t N, int32_t Ci, int32_t Co, void* out);

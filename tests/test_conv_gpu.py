@@ -100,7 +100,32 @@ def test_conv_order_invariance_bit_exact(pkg, dev, dtype):
     sorted_ = pkg.sparse_conv3d(f, w, None, m)
     rnd = torch.from_numpy(np.random.default_rng(1).permutation(n).astype(np.int32)).to(dev)
     shuffled = pkg.sparse_conv3d(f, w, None, m.nbr, order=rnd)
+    keyorder = pkg.sparse_conv3d(f, w, None, m.nbr, order=m.perm)
     assert torch.equal(ident, sorted_) and torch.equal(ident, shuffled)
+    assert torch.equal(ident, keyorder)
+
+
+@pytest.mark.parametrize("workload", ["map512", "wide128_bf16", "conv64_f32"])
+def test_map_conv_order(pkg, dev, workload):
+    """The conv order: inside each window of 16384 consecutive key-sorted rows, rows sorted by their
+    26-bit mask of present neighbors (tap 0 in the top bit, tap 13 left out), ties in key order."""
+    coords = pkg.workloads.make_coords(workload)
+    batch = int(coords[:, 0].max()) + 1
+    m = _map(pkg, dev, coords, batch, pkg.workloads.grid_shape(workload))
+    print(f"  conv order {workload} N={len(coords)}", flush=True)
+    order = m.conv_order().cpu().numpy()
+    perm = m.perm.cpu().numpy()
+    n = len(coords)
+    present = m.nbr.cpu().numpy() >= 0
+    m26 = np.zeros(n, np.int64)
+    for v in (v for v in range(27) if v != 13):
+        m26 = (m26 << 1) | present[:, v]
+    want = np.empty(n, np.int64)
+    win = 16384
+    for w0 in range(0, n, win):
+        rows = perm[w0:w0 + win]
+        want[w0:w0 + win] = rows[np.argsort(m26[rows], kind="stable")]
+    np.testing.assert_array_equal(order, want)
 
 
 def test_conv_properties(pkg, dev):

@@ -11,12 +11,12 @@ is not a Python identifier.
 from ._lib import TscError, load_library, header_symbols, LIB_PATH  # noqa: F401
 from .sparse_tensor import SparseTensor, Scale, Fraction, SCALE_IDENTITY, compute_layout  # noqa: F401
 from .conv3d import SparseConv3d, SparseResBlock3d, get_neighbor_map, neighbor_cache_key  # noqa: F401
-from .ops import (NeighborMap, build_neighbor_map, sparse_conv3d, layer_norm, silu, add,  # noqa: F401
-                  sparse_resblock)
+from .ops import (NeighborMap, build_neighbor_map, map_conv_order, sparse_conv3d,  # noqa: F401
+                  layer_norm, silu, add, sparse_resblock)
 from . import workloads  # noqa: F401
 
 __all__ = [
     "TscError", "SparseTensor", "SparseConv3d", "SparseResBlock3d", "NeighborMap",
-    "build_neighbor_map", "sparse_conv3d", "layer_norm", "silu", "add", "sparse_resblock",
+    "build_neighbor_map", "map_conv_order", "sparse_conv3d", "layer_norm", "silu", "add", "sparse_resblock",
     "get_neighbor_map", "neighbor_cache_key", "workloads",
 ]

@@ -287,6 +287,18 @@ int tsc_map_build(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t B, int
                           status_dev);
 }
 
+int tsc_map_conv_order(tsc_ctx* ctx, const int32_t* nbr, const int32_t* perm, int64_t N,
+                       int32_t* order_out) {
+  g_err[0] = 0;
+  int st = check_ctx(ctx);
+  if (st) return st;
+  if (N < 0 || N > INT32_MAX)
+    return fail(TSC_ERR_INVALID, "map_conv_order: N=%lld out of range", (long long)N);
+  if (N > 0 && (!nbr || !order_out)) return fail(TSC_ERR_INVALID, "map_conv_order: null nbr/order");
+  DeviceGuard g(ctx->device);
+  return tsc::conv_order_launch(ctx, nbr, perm, N, order_out);
+}
+
 int tsc_conv(tsc_ctx* ctx, int32_t dtype, const void* feats, const void* weight, const void* bias,
              const int32_t* nbr, const int32_t* order, int64_t N, int32_t Ci, int32_t Co,
              void* out) {

@@ -607,14 +607,13 @@ int launch_reg(tsc_ctx* ctx, const ConvArgs& a) {
   return check_hip(hipGetLastError(), "conv launch");
 }
 
-template <typename T, int BM, int BN, int KB, int WM, int WN, int EPI>
+template <typename T, int BM, int BN, int KB, int WM, int WN, int EPI, int BPC = 2>
 int launch_cfg(tsc_ctx* ctx, const ConvArgs& a) {
-  // Ring stages: as many as fit beside the neighbor tile in half of the 160 KB of LDS per CU, so
-  // that two blocks (eight waves) share a CU and one block's memory stalls overlap the other's
-  // MFMAs; at most 8.
+  // Ring stages: as many as fit beside the neighbor tile in 1/BPC of the 160 KB of LDS per CU
+  // (BPC blocks share a CU, so one block's memory stalls overlap another's MFMAs); at most 8.
   constexpr int STAGE = (BM + BN) * KB;
   constexpr int FIXED = BM * kTaps * 4 + BM * 4 + 256;
-  constexpr int FIT = (81408 - FIXED) / STAGE;
+  constexpr int FIT = (163840 / BPC - 512 - FIXED) / STAGE;
   constexpr int STAGES = FIT < 8 ? FIT : 8;
   static_assert(STAGES >= 2, "ring too shallow");
   const int32_t m_tiles = (int32_t)((a.N + BM - 1) / BM);
@@ -656,8 +655,13 @@ int dispatch_tiles(tsc_ctx* ctx, const ConvArgs& a) {
   // stage 32 epilogue rows of a 128-column half tile or a 64-column fp32 tile, so those shapes
   // take the next narrower tile.
   if constexpr (sizeof(T) < 4) {
+    if (a.Co % 256 == 0 && kb >= 64) {
+      // Widest channels: 256x256 tile, 2x4 waves of 128x64, one block per CU with a 4-stage
+      // ring (128 flops per LDS/L2 byte, 0.75 fragment reads per MFMA).
+      return launch_cfg<T, 256, 256, 64, 2, 4, EPI, 1>(ctx, a);
+    }
     if (a.Co % 128 == 0 && kb >= 64) {
-      // Wide channels: 128x128 tile, 2x2 waves of 64x64.
+      // Wide channels: 128x128 tile, 2x2 waves of 64x64, two blocks per CU.
       return launch_cfg<T, 128, 128, 64, 2, 2, EPI>(ctx, a);
     }
     if (a.Co % 64 == 0) {

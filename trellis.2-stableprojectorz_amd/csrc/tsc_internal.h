@@ -81,6 +81,10 @@ int map_build_radix(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t B, i
                     int32_t Y, int32_t Z, const int32_t dil[3], void* keys_out, int32_t* perm_out,
                     int32_t* nbr_out, uint32_t* status_dev);
 
+// ---- launcher implemented in conv_order.hip ----
+int conv_order_launch(tsc_ctx* ctx, const int32_t* nbr, const int32_t* perm, int64_t N,
+                      int32_t* order);
+
 // ---- launchers implemented in conv.hip ----
 struct ConvArgs {
   int32_t dtype;

@@ -53,6 +53,27 @@ class NeighborMap:
     spatial_shape: tuple
     batch_size: int
     dilation: tuple
+    _conv_order: torch.Tensor | None = None
+
+    def conv_order(self) -> torch.Tensor:
+        """Row order the convs use (tsc_map_conv_order), computed on first use and cached."""
+        if self._conv_order is None:
+            self._conv_order = map_conv_order(self.nbr, self.perm)
+        return self._conv_order
+
+
+def map_conv_order(nbr: torch.Tensor, perm: torch.Tensor | None = None) -> torch.Tensor:
+    """Rows grouped by their set of present neighbors inside windows of the sorted order."""
+    if nbr.dtype != torch.int32 or nbr.dim() != 2 or nbr.shape[1] != 27:
+        raise TscError(_lib.TSC_ERR_INVALID, "nbr must be int32 (N,27)")
+    n = nbr.shape[0]
+    if perm is not None and (perm.dtype != torch.int32 or perm.numel() != n):
+        raise TscError(_lib.TSC_ERR_INVALID, "perm must be int32 (N,)")
+    dev = _dev(nbr, perm)
+    ctx = _lib.context(dev)
+    order = torch.empty((n,), dtype=torch.int32, device=nbr.device)
+    check(ctx.lib.tsc_map_conv_order(ctx.bind(), _p(nbr), _p(perm), n, _p(order)))
+    return order
 
 
 def build_neighbor_map(coords: torch.Tensor, spatial_shape, batch_size: int,
@@ -95,7 +116,7 @@ def build_neighbor_map(coords: torch.Tensor, spatial_shape, batch_size: int,
 
 def _nbr_and_order(nmap, order):
     if isinstance(nmap, NeighborMap):
-        return nmap.nbr, (nmap.perm if order is None else order)
+        return nmap.nbr, (nmap.conv_order() if order is None else order)
     return nmap, order
 
 
