@@ -631,6 +631,228 @@ int launch_cfg(tsc_ctx* ctx, const ConvArgs& a) {
   return check_hip(hipGetLastError(), "conv launch");
 }
 
+// Narrow-channel kernel (16-bit types, Ci = 32: one 64-byte row per neighbor).  Every wave works
+// alone on tiles of 32 output rows; there is no block barrier after the weights are staged.  The
+// design minimises distinct cache lines per memory instruction, which bounds the L1/TA rate of
+// gather-heavy code:
+//   rows      the 32 rows of the tile (entries of `order`); their 32 x 27 neighbor indices are
+//             read with consecutive lanes on consecutive words of each 108-byte row and parked in
+//             the wave's LDS slice as [tap][row]; an OR-reduction gives the tile's tap mask.
+//   taps      only the tile's taps are visited; a ring of R slots holds the gathered feature
+//             rows of the next R taps, 16 bytes per lane: in v_mfma_f32_16x16x32 B-operand order
+//             lanes l, l+16, l+32, l+48 hold the four 16-byte pieces of row l%16, so one load
+//             instruction fetches 16 whole rows (an absent neighbor reads the zero block).
+//   MFMA      transposed product D[co][row] = W[co][k] * F[row][k]: A = weight fragment from LDS
+//             (the (Co,27,Ci) tensor is staged once per block, 16-byte pieces XOR-swizzled per
+//             row), B = the gathered rows.  Two 16-row blocks x Co/16 column blocks per tap.
+//   epilogue  lane l owns row 16*rb + l%16 and co 16*cb + 4*(l/16) + {0..3}: bias (+ residual)
+//             in fp32, one rounding, 8-byte stores.
+// Tiles are dealt XCD-contiguously: XCD x owns tiles [x*tpx, (x+1)*tpx), so each XCD's L2 sees one
+// spatial region of gathered rows.
+constexpr int kNarrowSlots = 4;
+typedef float f32x4_t __attribute__((__vector_size__(4 * sizeof(float))));
+
+template <typename T>
+__device__ __forceinline__ void mfma16_piece(const uint4& a, const uint4& b, f32x4_t& acc);
+template <>
+__device__ __forceinline__ void mfma16_piece<__bf16>(const uint4& a, const uint4& b,
+                                                     f32x4_t& acc) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                __builtin_bit_cast(bf16x8_t, b), acc, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ void mfma16_piece<_Float16>(const uint4& a, const uint4& b,
+                                                       f32x4_t& acc) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                               __builtin_bit_cast(f16x8_t, b), acc, 0, 0, 0);
+}
+
+template <typename T, int CO, int EPI, int NT>
+__global__ void __launch_bounds__(NT)
+    conv_narrow_kernel(const T* __restrict__ feats, const T* __restrict__ weight,
+                       const T* __restrict__ bias, const int32_t* __restrict__ nbr,
+                       const int32_t* __restrict__ order, int64_t N, int32_t n_tiles,
+                       int32_t tiles_per_xcd, const T* residual, T* out) {
+  constexpr int CI = 32;
+  constexpr int PPR = 4;            // 16-byte pieces per weight / feature row
+  constexpr int CB = CO / 16;       // 16-column output blocks
+  constexpr int NW = NT / 64;
+  constexpr int R = kNarrowSlots;
+  static_assert(CO % 16 == 0, "narrow kernel: Co multiple of 16");
+  __shared__ uint4 sW[kTaps * CO * PPR];
+  __shared__ int32_t sNb[NW][kTaps * 32];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int l16 = lane & 15, q = lane >> 4;
+
+  // Stage W (Co,27,Ci): global piece g = (co*27 + v)*PPR + p  ->  LDS [(v*CO + co)*PPR + swz(p)].
+  const uint4* wq = (const uint4*)weight;
+  for (int g = tid; g < CO * kTaps * PPR; g += NT) {
+    const int p = g % PPR, cv = g / PPR, v = cv % kTaps, co = cv / kTaps;
+    sW[(v * CO + co) * PPR + swz<PPR>(co, p)] = wq[g];
+  }
+  __syncthreads();
+  int32_t* const nbw = sNb[wid];
+
+  const int xcd = blockIdx.x & 7;
+  const int t_begin = xcd * tiles_per_xcd;
+  const int t_end = min(n_tiles, t_begin + tiles_per_xcd);
+  const int stride = (int)(gridDim.x >> 3) * NW;
+  // Tiles are software-pipelined: while tile t computes, the neighbor indices of tile t+1 and
+  // the row numbers of tile t+2 are in flight, so a tile starts without a dependent round trip.
+  // Neighbor indices: iteration it reads rows 2*it and 2*it+1 with lanes 0-26 and 27-53 on
+  // consecutive words of each 108-byte row; they land in the wave's LDS slice as [row][tap]
+  // (odd row stride: the slot fills' 16-lane reads of one tap hit distinct banks).
+  const int lv = lane % kTaps, lr = lane / kTaps;  // lr = 2 for the idle lanes 54-63
+  auto load_row = [&](int t) -> int32_t {
+    const int64_t pos = (int64_t)t * 32 + (lane & 31);
+    return (t < t_end && pos < N) ? (order ? order[pos] : (int32_t)pos) : -1;
+  };
+  int32_t val[16];
+  auto load_nbr = [&](int32_t rows) {
+#pragma unroll
+    for (int it = 0; it < 16; ++it) {
+      const int32_t row = __shfl(rows, (2 * it + lr) & 31, 64);
+      val[it] = (lr < 2 && row >= 0) ? nbr[(int64_t)row * kTaps + lv] : -1;
+    }
+  };
+  int tile = t_begin + (int)(blockIdx.x >> 3) * NW + wid;
+  int32_t my_row = load_row(tile);
+  int32_t row_next = load_row(tile + stride);
+  load_nbr(my_row);
+  for (; tile < t_end; tile += stride) {
+#pragma unroll
+    for (int it = 0; it < 16; ++it)
+      if (lr < 2) nbw[(2 * it + lr) * kTaps + lv] = val[it];
+    load_nbr(row_next);
+    const int32_t row_after = load_row(tile + 2 * stride);
+    // Tap mask: lane l < 54 ORs tap l % 27 over rows [16*(l/27), 16*(l/27)+16).
+    uint32_t mymask = 0;
+    if (lane < 2 * kTaps) {
+      const int v = lane % kTaps, r0 = (lane / kTaps) * 16;
+      bool any = false;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) any |= nbw[(r0 + r) * kTaps + v] >= 0;
+      mymask = any ? 1u << v : 0u;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mymask |= __shfl_xor(mymask, off, 64);
+    const uint32_t tmask = __builtin_amdgcn_readfirstlane(mymask);
+    const int ntaps = __popc(tmask);
+
+    f32x4_t acc[2][CB];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[rb][cb][e] = 0.f;
+
+    // Slot ring: slot r holds tap vt[r] (-1 past the last tap: zero-block pieces, never used).
+    uint32_t rem = tmask;
+    int vt[R];
+    uint4 fr[R][2];
+    // Loads are coalesced (lanes 4j..4j+3 read the four pieces of row 16*rb + j, one 64-byte
+    // request per row); the fragment the MFMA wants in lane t (row t%16, piece t/16) is then
+    // fetched from lane 4*(t%16) + t/16 with ds_bpermute right before use.
+    auto fill = [&](int r) {
+      const int v = rem ? __builtin_ctz(rem) : -1;
+      rem &= rem - 1u;
+      vt[r] = v;
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) {
+        const int32_t sidx = v >= 0 ? nbw[(rb * 16 + (lane >> 2)) * kTaps + v] : -1;
+        const T* src = sidx >= 0 ? feats + (int64_t)sidx * CI + (lane & 3) * 8
+                                 : (const T*)g_zero + (lane & 3) * 8;
+        fr[r][rb] = *(const uint4*)src;
+      }
+    };
+    const int src_lane = 4 * l16 + q;
+    auto to_mfma = [&](const uint4& x) {
+      uint4 y;
+      y.x = __shfl(x.x, src_lane, 64);
+      y.y = __shfl(x.y, src_lane, 64);
+      y.z = __shfl(x.z, src_lane, 64);
+      y.w = __shfl(x.w, src_lane, 64);
+      return y;
+    };
+#pragma unroll
+    for (int r = 0; r < R; ++r) fill(r);
+    for (int t0 = 0; t0 < ntaps; t0 += R) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        if (t0 + r < ntaps) {
+          const int v = vt[r];
+          const uint4 b0 = to_mfma(fr[r][0]), b1 = to_mfma(fr[r][1]);
+#pragma unroll
+          for (int cb = 0; cb < CB; ++cb) {
+            const int co = cb * 16 + l16;
+            const uint4 wa = sW[(v * CO + co) * PPR + swz<PPR>(co, q)];
+            mfma16_piece<T>(wa, b0, acc[0][cb]);
+            mfma16_piece<T>(wa, b1, acc[1][cb]);
+          }
+        }
+        fill(r);
+      }
+    }
+
+    // Epilogue.
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      const int32_t row = __shfl(my_row, rb * 16 + l16, 64);
+      if (row < 0) continue;
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) {
+        const int c0 = cb * 16 + 4 * q;
+        float x[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[i] = acc[rb][cb][i];
+        if (bias) {
+          const uint2 bb = *(const uint2*)(bias + c0);
+          const T* bt = (const T*)&bb;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) x[i] += to_f32<T>(bt[i]);
+        }
+        if (EPI == TSC_EPI_BIAS_RESIDUAL) {
+          const uint2 rr = *(const uint2*)(residual + (int64_t)row * CO + c0);
+          const T* rt = (const T*)&rr;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) x[i] += to_f32<T>(rt[i]);
+        }
+        T y[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) y[i] = from_f32<T>(x[i]);
+        *(uint2*)(out + (int64_t)row * CO + c0) = *(const uint2*)y;
+      }
+    }
+    my_row = row_next;
+    row_next = row_after;
+  }
+}
+
+template <typename T, int CO, int EPI>
+int launch_narrow(tsc_ctx* ctx, const ConvArgs& a) {
+  // Block size: 8 waves (one block per CU) when the weights + per-wave neighbor slices fit.
+  // Measured on the 1.5M-voxel shell: 8 waves beat 16 (fewer concurrent gathers thrash the
+  // L1/L2 less) and 4 (too little memory-level parallelism).
+  constexpr int kW = kTaps * CO * 4 * 16;
+  constexpr int kPerWave = kTaps * 32 * 4;
+  constexpr int NW = std::min(8, (163840 - 1024 - kW) / kPerWave);
+  static_assert(NW >= 4, "narrow kernel: weights too large for LDS");
+  constexpr int NT = NW * 64;
+  const int32_t n_tiles = (int32_t)((a.N + 31) / 32);
+  const int32_t tpx = (n_tiles + 7) / 8;
+  int32_t blocks = std::min<int32_t>(256, (n_tiles + NW - 1) / NW);
+  blocks = std::max<int32_t>(8, (blocks + 7) / 8 * 8);
+  static const std::string name = std::string("conv_narrow_") +
+      (std::is_same<T, __bf16>::value ? "bf16" : "f16") + "_32x" + std::to_string(CO) +
+      (EPI == TSC_EPI_BIAS_RESIDUAL ? "_res" : "");
+  ProfScope p(ctx, name.c_str());
+  conv_narrow_kernel<T, CO, EPI, NT><<<blocks, NT, 0, ctx->stream>>>(
+      (const T*)a.feats, (const T*)a.weight, (const T*)a.bias, a.nbr, a.order, a.N, n_tiles, tpx,
+      (const T*)a.residual, (T*)a.out);
+  return check_hip(hipGetLastError(), "conv launch");
+}
+
 // Largest chunk (bytes per row) that divides the Ci row and is a multiple of 32 bytes.
 inline int pick_kb(int row_bytes) {
   if (row_bytes % 128 == 0) return 128;
@@ -641,8 +863,13 @@ inline int pick_kb(int row_bytes) {
 template <typename T, int EPI>
 int dispatch_tiles(tsc_ctx* ctx, const ConvArgs& a) {
   const int kb = pick_kb(a.Ci * (int)sizeof(T));
+  if constexpr (sizeof(T) == 2) {
+    // Narrow 16-bit rows: wave-level gather tiles (weights in LDS).
+    if (a.Ci == 32 && a.Co == 32) return launch_narrow<T, 32, EPI>(ctx, a);
+    if (a.Ci == 32 && a.Co == 64) return launch_narrow<T, 64, EPI>(ctx, a);
+  }
   if (a.Ci * (int)sizeof(T) <= 64) {
-    // Narrow input rows: one K chunk per tap -> register-staged double buffer.
+    // Other narrow input rows: one K chunk per tap -> register-staged double buffer.
     if (a.Co % 64 == 0) {
       if (kb == 64) return launch_reg<T, 128, 64, 64, 4, 1, EPI>(ctx, a);
       return launch_reg<T, 128, 64, 32, 4, 1, EPI>(ctx, a);
