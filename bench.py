@@ -287,6 +287,9 @@ def main() -> int:
                 "kernels": {k: {"avg_ms": round(a, 4), "launches_per_step": c} for k, (a, c) in kt.items()}}
     log(f"dominant kernel {dom}: {dom_ms:.4f} ms; all: " +
         ", ".join(f"{k}={a:.4f}" for k, (a, c) in kt.items()))
+    # One-time per coordinate set, cached with the map: the row order the convs use.
+    order_ms = time_steps(lambda: pkg.map_conv_order(nmap.nbr, nmap.perm), args.steps, args.warmup)
+    log(f"conv row order (tsc_map_conv_order): {order_ms:.4f} ms")
     del nmap
     sec = []
     if not args.no_secondary:
@@ -305,7 +308,11 @@ def main() -> int:
                                f"ellipsoid in 512^3, shuffled rows, 3x3x3 dilation 1",
                    "voxels": n, "grid": list(shape), "batch": 1,
                    "bytes_per_voxel_algorithmic": MAP_BYTES_PER_VOXEL},
-        "roofline": roofline, "cpu_baseline": cpu, "secondary": sec,
+        "roofline": roofline, "cpu_baseline": cpu,
+        "map_prep": {"conv_order_ms": round(order_ms, 4),
+                     "note": "tsc_map_conv_order, once per coordinate set (cached with the map); "
+                             "not part of ms_per_step"},
+        "secondary": sec,
     }
     print(json.dumps(line), flush=True)
     return 0

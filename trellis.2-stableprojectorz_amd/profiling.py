@@ -8,7 +8,7 @@
       same counters on a device copy of --calib-bytes bytes (the largest copy dispatch in the run)
 
 Kernel names are shortened to the name the library's own profiler uses where possible
-(e.g. conv_mfma_kernel<__bf16,128,128,128,3,2,2,0> -> conv_mfma_kernel<bf16,128x128,k128,s3>).
+(e.g. conv_mfma_kernel<__bf16,256,256,64,4,2,4,0> -> conv_mfma_kernel<bf16,256x256,k64,s4>).
 """
 from __future__ import annotations
 
@@ -21,16 +21,29 @@ from collections import defaultdict
 _TYPES = {"DF16b": "bf16", "DF16_": "f16", "f": "f32"}
 
 
+_DEMANGLED_TYPES = {"__bf16": "bf16", "_Float16": "f16", "float": "f32"}
+
+
+def _conv_name(kind: str, t: str, nums: list) -> str:
+    if kind == "conv_mfma_kernel":  # BM, BN, KB, STAGES, WM, WN, EPI
+        bm, bn, kb, st, _, _, epi = nums
+        return f"conv_mfma_kernel<{t},{bm}x{bn},k{kb},s{st}{',res' if epi == '1' else ''}>"
+    if kind == "conv_narrow_kernel":  # CO, EPI, threads
+        co, epi, _ = nums
+        return f"conv_narrow_kernel<{t},32x{co}{',res' if epi == '1' else ''}>"
+    bm, bn, kb, _, _, epi = nums  # conv_regstage_kernel
+    return f"conv_regstage_kernel<{t},{bm}x{bn},k{kb}{',res' if epi == '1' else ''}>"
+
+
 def short_name(name: str) -> str:
-    m = re.search(r"(conv_mfma_kernel|conv_regstage_kernel)I(DF16b|DF16_|f)((?:Li\d+E)+)", name)
+    kinds = "conv_mfma_kernel|conv_regstage_kernel|conv_narrow_kernel"
+    m = re.search(rf"({kinds})I(DF16b|DF16_|f)((?:Li\d+E)+)", name)  # mangled
     if m:
-        nums = re.findall(r"Li(\d+)E", m.group(3))
-        t = _TYPES[m.group(2)]
-        if m.group(1) == "conv_mfma_kernel":  # BM, BN, KB, STAGES, WM, WN, EPI
-            bm, bn, kb, st, _, _, epi = nums
-            return f"conv_mfma_kernel<{t},{bm}x{bn},k{kb},s{st}{',res' if epi == '1' else ''}>"
-        bm, bn, kb, _, _, epi = nums
-        return f"conv_regstage_kernel<{t},{bm}x{bn},k{kb}{',res' if epi == '1' else ''}>"
+        return _conv_name(m.group(1), _TYPES[m.group(2)], re.findall(r"Li(\d+)E", m.group(3)))
+    m = re.search(rf"({kinds})<(__bf16|_Float16|float), ([\d, ]+)>", name)  # demangled
+    if m:
+        return _conv_name(m.group(1), _DEMANGLED_TYPES[m.group(2)],
+                          [x.strip() for x in m.group(3).split(",")])
     m = re.search(r"(?:tsc::\(anonymous namespace\)::|N_1\d+)(\w+_kernel)", name)
     if m:
         base = m.group(1)
