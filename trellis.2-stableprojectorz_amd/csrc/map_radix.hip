@@ -3,7 +3,7 @@
 // Same outputs as the bitmap path (sorted unique keys, their rows, the (N,27) neighbor table; see
 // map_build.hip for the semantics and reference citations).  Keys have nbits = bitlen(cells-1)
 // bits; the top TB = min(nbits, 10) bits select one of 2^TB buckets.  Steps:
-//   pack       coords -> (key, row) in input order, per-4096-tile histogram of the bucket digit
+//   pack       coords -> (key, row) in input order, per-8192-row tile histogram of the bucket digit
 //              and a per-tile out-of-range flag.  Out-of-range coordinates are clamped to the
 //              last cell (so every key stays below 2^nbits) and reported through the flag.
 //   scan       exclusive scan over tiles of each bucket's counts (one block per bucket), bucket
@@ -36,7 +36,8 @@ constexpr int LBITS = 9;            // local pass digit bits
 constexpr int LNB = 1 << LBITS;
 constexpr int LPT = LNB / RT;       // local digits owned per thread
 constexpr int PT = 512;             // pack / partition threads per block
-constexpr int PI = RTILE / PT;      // pack / partition items per thread
+constexpr int PI = 16;              // pack / partition items per thread
+constexpr int PTILE = PT * PI;      // pack / partition tile
 constexpr int PDPT = NBMAX / PT;    // bucket digits owned per thread in the partition prefix
 
 template <typename K>
@@ -58,7 +59,7 @@ __global__ void __launch_bounds__(PT)
   const int nb = 1 << dbits, mask = nb - 1;
   for (int d = threadIdx.x; d < nb; d += PT) hist[d] = 0;
   __syncthreads();
-  const int64_t base = (int64_t)blockIdx.x * RTILE;
+  const int64_t base = (int64_t)blockIdx.x * PTILE;
   int oob = 0;
 #pragma unroll
   for (int j = 0; j < PI; ++j) {
@@ -176,13 +177,13 @@ __global__ void __launch_bounds__(PT)
   __shared__ int dstart[NBMAX];
   __shared__ int gbase[NBMAX];
   __shared__ int wsum[PT / 64];
-  __shared__ K sk[RTILE];
-  __shared__ int32_t sv[RTILE];
+  __shared__ K sk[PTILE];
+  __shared__ int32_t sv[PTILE];
   const int nb = 1 << dbits, mask = nb - 1;
   const int tid = threadIdx.x;
   for (int i = tid; i < NBMAX; i += PT) lcnt[i] = 0;
   __syncthreads();
-  const int64_t tile0 = (int64_t)blockIdx.x * RTILE;
+  const int64_t tile0 = (int64_t)blockIdx.x * PTILE;
   K kk[PI];
   int32_t vv[PI];
   int slot[PI];
@@ -235,7 +236,7 @@ __global__ void __launch_bounds__(PT)
   }
   __syncthreads();
   const int64_t rem = N - tile0;
-  const int tile_n = rem < RTILE ? (int)rem : RTILE;
+  const int tile_n = rem < PTILE ? (int)rem : PTILE;
   for (int i = tid; i < tile_n; i += PT) {
     const K k = sk[i];
     const int d = digit_of<K>(k, shift, mask);
@@ -512,8 +513,8 @@ struct ColumnLookup {
 // most 2*dW + 1 consecutive entries.  A kd window that does not fit (very sparse or very dense
 // regions) falls back to the global column lookup for that kd only.
 constexpr int kWinThreads = 256;
-constexpr int kWinRounds = 8;
-constexpr int kWinVox = kWinRounds * mapk::kFillVoxPerWave * (kWinThreads / 64);  // 224
+constexpr int kWinRounds = 4;
+constexpr int kWinVox = kWinRounds * mapk::kFillVoxPerWave * (kWinThreads / 64);  // 112
 constexpr int kWinCapE = 464;  // voxels per kd window
 constexpr int kWinCapC = 432;  // columns per kd window (LDS < 20 KB per block: 8 blocks per CU)
 
@@ -740,7 +741,7 @@ int radix_impl(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t B, int32_
   const int tb = std::min(nbits, TBMAX);
   const int lb = nbits - tb;
   const int nbk = 1 << tb;
-  const int64_t ntiles = (N + RTILE - 1) / RTILE;
+  const int64_t ntiles = (N + PTILE - 1) / PTILE;
   const int64_t ncol = (int64_t)B * X * Y;
   const bool use_cols = ncol <= std::max<int64_t>(16 * N, int64_t(1) << 22);
   const int64_t S = (int64_t)nbk * ntiles;
