@@ -897,6 +897,10 @@ int dispatch_tiles(tsc_ctx* ctx, const ConvArgs& a) {
       return launch_cfg<T, 128, 64, 32, 4, 1, EPI>(ctx, a);
     }
   } else {
+    // Small problems (fewer 128-row tiles than CUs, e.g. ~25k voxels): 64x64 tiles of four
+    // 32x32 waves so every CU gets work.
+    if (a.Co % 64 == 0 && kb >= 128 && ((a.N + 127) / 128) * (a.Co / 64) < 256)
+      return launch_cfg<T, 64, 64, 128, 2, 2, EPI>(ctx, a);
     if (a.Co % 64 == 0 && kb >= 64) return launch_cfg<T, 128, 64, 64, 4, 1, EPI>(ctx, a);
   }
   // Co % 32 == 0
