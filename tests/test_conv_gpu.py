@@ -107,7 +107,7 @@ def test_conv_order_invariance_bit_exact(pkg, dev, dtype):
 
 @pytest.mark.parametrize("workload", ["map512", "wide128_bf16", "conv64_f32"])
 def test_map_conv_order(pkg, dev, workload):
-    """The conv order: inside each window of 16384 consecutive key-sorted rows, rows sorted by their
+    """The conv order: inside each window of 65536 consecutive key-sorted rows, rows sorted by their
     26-bit mask of present neighbors (tap 0 in the top bit, tap 13 left out), ties in key order."""
     coords = pkg.workloads.make_coords(workload)
     batch = int(coords[:, 0].max()) + 1
@@ -121,7 +121,7 @@ def test_map_conv_order(pkg, dev, workload):
     for v in (v for v in range(27) if v != 13):
         m26 = (m26 << 1) | present[:, v]
     want = np.empty(n, np.int64)
-    win = 16384
+    win = 65536
     for w0 in range(0, n, win):
         rows = perm[w0:w0 + win]
         want[w0:w0 + win] = rows[np.argsort(m26[rows], kind="stable")]

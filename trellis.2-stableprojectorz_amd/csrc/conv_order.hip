@@ -1,17 +1,26 @@
 // Row order for the conv kernels: rows sorted by their set of present neighbors.
 //
-// The conv kernels process output rows in tiles (32 or 128 consecutive entries of `order`) and
+// The conv kernels process output rows in tiles (32 to 256 consecutive entries of `order`) and
 // skip a tap only when no row of the tile has that neighbor.  In key order a tile of a thin
 // shell touches nearly all 27 taps although each row has ~9-17 neighbors, so most tap work is
-// multiplication by absent (zero) rows.  This kernel sorts rows inside windows of kOrdWin
+// multiplication by absent (zero) rows.  The order sorts rows inside windows of kOrdWin = 65536
 // consecutive key-sorted rows (spatially compact, so gathers stay local) by their 26-bit mask of
 // present neighbors (tap 0 in the top bit; tap 13, the row itself, is always present): numeric
 // order puts masks that share their leading taps next to each other, so a tile's union of taps
-// stays close to one row's.  One block per window: the masks and window positions (uint16) sit
-// in LDS and three stable LSD passes of <= 9 bits rank them with wave ballots (peer mask per
-// digit, popcount of lower peers + the wave's running count, cross-wave offsets per digit).
+// stays close to one row's.  Ties keep key order.
+//
+// Stable LSD radix sort, three passes of <= 9 bits, over tiles of 16384 rows (4 per window):
+//   mask     key = mask of row perm[i], val = perm[i]; tile histogram of digit 0
+//   scan     per window: digit-major, tile-minor exclusive offsets of the 4 tiles' counts
+//   scatter  per tile: wave-ballot stable ranks (one ballot per digit bit -> peer mask; popcount
+//            of lower peers + the wave's running count; per-digit offsets across waves), written
+//            to window start + offset of (tile, digit) + rank
+//   hist     tile histogram of the next digit
 // Measured utilisation (valid taps / processed taps) on the thin shells: key order 0.37 (1-voxel
-// shell, 32-row tiles) and 0.61 (2-voxel shells, 128-row tiles); sorted windows 0.81 and 0.72.
+// shell, 32-row tiles) and 0.61 (2-voxel shells, 256-row tiles); sorted 65536-row windows 0.91
+// and 0.74.
+
+#include <utility>
 
 #include "tsc_internal.h"
 
@@ -20,13 +29,15 @@ namespace {
 
 constexpr int kOrdThreads = 1024;
 constexpr int kOrdItems = 16;
-constexpr int kOrdWin = kOrdThreads * kOrdItems;  // 16384 rows per window
+constexpr int kOrdTile = kOrdThreads * kOrdItems;  // 16384 rows per tile
+constexpr int kOrdTilesPerWin = 4;                 // 65536 rows per window
 constexpr int kOrdWaves = kOrdThreads / 64;
 constexpr int kOrdDigitBits = 9;
 constexpr int kOrdBins = 1 << kOrdDigitBits;
 constexpr int kOrdMaskBits = 26;
+constexpr int kOrdPasses = (kOrdMaskBits + kOrdDigitBits - 1) / kOrdDigitBits;
 
-__device__ __forceinline__ int block_excl_scan_1024(int v, int* wsum) {
+__device__ __forceinline__ int block_excl_scan(int v, int* wsum, int nw) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   int incl = v;
 #pragma unroll
@@ -37,104 +48,154 @@ __device__ __forceinline__ int block_excl_scan_1024(int v, int* wsum) {
   if (lane == 63) wsum[w] = incl;
   __syncthreads();
   int pre = incl - v;
-  for (int ww = 0; ww < w; ++ww) pre += wsum[ww];
+  for (int ww = 0; ww < w && ww < nw; ++ww) pre += wsum[ww];
   __syncthreads();
   return pre;
 }
 
+__device__ __forceinline__ int digit(uint32_t k, int shift) {
+  return (int)((k >> shift) & (uint32_t)(kOrdBins - 1));
+}
+
 __global__ void __launch_bounds__(kOrdThreads)
-    conv_order_kernel(const int32_t* __restrict__ nbr, const int32_t* __restrict__ perm,
-                      int64_t n, int32_t* __restrict__ order) {
-  __shared__ uint32_t skey[kOrdWin];
-  __shared__ uint16_t spos[kOrdWin];
-  __shared__ int wcnt[kOrdWaves][kOrdBins];
-  __shared__ int run[kOrdBins];
-  __shared__ int wsum[kOrdWaves];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int64_t w0 = (int64_t)blockIdx.x * kOrdWin;
-  const int size = (int)((n - w0) < kOrdWin ? (n - w0) : kOrdWin);
-  for (int i = tid; i < size; i += kOrdThreads) {
-    const int32_t r = perm ? perm[w0 + i] : (int32_t)(w0 + i);
-    const int32_t* nr = nbr + (int64_t)r * 27;
-    uint32_t m = 0;
+    ord_mask_kernel(const int32_t* __restrict__ nbr, const int32_t* __restrict__ perm,
+                    int64_t n, uint32_t* __restrict__ keys, int32_t* __restrict__ vals,
+                    int* __restrict__ counts) {
+  __shared__ int hist[kOrdBins];
+  const int tid = threadIdx.x;
+  for (int d = tid; d < kOrdBins; d += kOrdThreads) hist[d] = 0;
+  __syncthreads();
+  const int64_t t0 = (int64_t)blockIdx.x * kOrdTile;
+#pragma unroll 4
+  for (int j = 0; j < kOrdItems; ++j) {
+    const int64_t i = t0 + j * kOrdThreads + tid;
+    if (i < n) {
+      const int32_t r = perm ? perm[i] : (int32_t)i;
+      const int32_t* nr = nbr + (int64_t)r * 27;
+      uint32_t m = 0;
 #pragma unroll
-    for (int v = 0; v < 27; ++v) {
-      if (v == 13) continue;
-      m = (m << 1) | (uint32_t)(nr[v] >= 0);
+      for (int v = 0; v < 27; ++v) {
+        if (v == 13) continue;
+        m = (m << 1) | (uint32_t)(nr[v] >= 0);
+      }
+      keys[i] = m;
+      vals[i] = r;
+      atomicAdd(&hist[digit(m, 0)], 1);
     }
-    skey[i] = m;
-    spos[i] = (uint16_t)i;
   }
-  // Wave w ranks the contiguous run [w*ipw*64, (w+1)*ipw*64) of the window.
+  __syncthreads();
+  for (int d = tid; d < kOrdBins; d += kOrdThreads) counts[blockIdx.x * kOrdBins + d] = hist[d];
+}
+
+__global__ void __launch_bounds__(kOrdThreads)
+    ord_hist_kernel(const uint32_t* __restrict__ keys, int64_t n, int shift,
+                    int* __restrict__ counts) {
+  __shared__ int hist[kOrdBins];
+  const int tid = threadIdx.x;
+  for (int d = tid; d < kOrdBins; d += kOrdThreads) hist[d] = 0;
+  __syncthreads();
+  const int64_t t0 = (int64_t)blockIdx.x * kOrdTile;
+#pragma unroll 4
+  for (int j = 0; j < kOrdItems; ++j) {
+    const int64_t i = t0 + j * kOrdThreads + tid;
+    if (i < n) atomicAdd(&hist[digit(keys[i], shift)], 1);
+  }
+  __syncthreads();
+  for (int d = tid; d < kOrdBins; d += kOrdThreads) counts[blockIdx.x * kOrdBins + d] = hist[d];
+}
+
+// One block per window, thread = digit: offs[t][d] = (elements of smaller digits in the window)
+// + (digit d in the window's earlier tiles).
+__global__ void __launch_bounds__(kOrdBins)
+    ord_scan_kernel(const int* __restrict__ counts, int ntiles, int* __restrict__ offs) {
+  __shared__ int wsum[kOrdBins / 64];
+  const int d = threadIdx.x;
+  const int tb = blockIdx.x * kOrdTilesPerWin;
+  const int nt = min(kOrdTilesPerWin, ntiles - tb);
+  int c[kOrdTilesPerWin], tot = 0;
+#pragma unroll
+  for (int t = 0; t < kOrdTilesPerWin; ++t) {
+    c[t] = t < nt ? counts[(tb + t) * kOrdBins + d] : 0;
+    tot += c[t];
+  }
+  int run = block_excl_scan(tot, wsum, kOrdBins / 64);
+#pragma unroll
+  for (int t = 0; t < kOrdTilesPerWin; ++t) {
+    if (t < nt) offs[(tb + t) * kOrdBins + d] = run;
+    run += c[t];
+  }
+}
+
+// Stable scatter of one tile.  Wave w ranks the contiguous run [w*ipw*64, (w+1)*ipw*64) of the
+// tile item by item (lanes = consecutive elements), so element order = (wave, item, lane).
+__global__ void __launch_bounds__(kOrdThreads)
+    ord_scatter_kernel(const uint32_t* __restrict__ ksrc, const int32_t* __restrict__ vsrc,
+                       int64_t n, int shift, int dbits, const int* __restrict__ offs,
+                       uint32_t* __restrict__ kdst, int32_t* __restrict__ vdst) {
+  __shared__ int wcnt[kOrdWaves][kOrdBins];
+  __shared__ int start[kOrdBins];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t t0 = (int64_t)blockIdx.x * kOrdTile;
+  const int64_t win0 = (int64_t)(blockIdx.x / kOrdTilesPerWin) * kOrdTilesPerWin * kOrdTile;
+  const int size = (int)((n - t0) < kOrdTile ? (n - t0) : kOrdTile);
+  for (int i = tid; i < kOrdWaves * kOrdBins; i += kOrdThreads) (&wcnt[0][0])[i] = 0;
+  for (int d = tid; d < kOrdBins; d += kOrdThreads) start[d] = offs[blockIdx.x * kOrdBins + d];
+  __syncthreads();
   const int ipw = ((size + 63) / 64 + kOrdWaves - 1) / kOrdWaves;
   const int wfirst = w * ipw * 64;
   const int wlimit = min(size, wfirst + ipw * 64);
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  constexpr int passes = (kOrdMaskBits + kOrdDigitBits - 1) / kOrdDigitBits;
-  for (int p = 0; p < passes; ++p) {
-    const int shift = p * kOrdDigitBits;
-    const int dbits = min(kOrdDigitBits, kOrdMaskBits - shift);
-    const int mask = (1 << dbits) - 1;
-    for (int i = tid; i < kOrdWaves * kOrdBins; i += kOrdThreads) (&wcnt[0][0])[i] = 0;
-    __syncthreads();
-    uint32_t kk[kOrdItems];
-    uint16_t pp[kOrdItems];
-    int lr[kOrdItems];
+  const int mask = (1 << dbits) - 1;
+  uint32_t kk[kOrdItems];
+  int32_t vv[kOrdItems];
+  int lr[kOrdItems];
 #pragma unroll
-    for (int j = 0; j < kOrdItems; ++j) {
-      const int e = wfirst + j * 64 + lane;
-      const bool valid = e < wlimit;
-      kk[j] = valid ? skey[e] : 0u;
-      pp[j] = valid ? spos[e] : (uint16_t)0;
-    }
-#pragma unroll
-    for (int j = 0; j < kOrdItems; ++j) {
-      lr[j] = 0;
-      if (j >= ipw) continue;  // uniform
-      const bool valid = wfirst + j * 64 + lane < wlimit;
-      const int d = (int)((kk[j] >> shift) & (uint32_t)mask);
-      uint64_t peers = __ballot(valid);
-      for (int b = 0; b < dbits; ++b) {
-        const bool bit = (d >> b) & 1;
-        const uint64_t mb = __ballot(valid && bit);
-        peers &= bit ? mb : ~mb;
-      }
-      if (valid) {
-        const int before = __popcll(peers & lt_mask);
-        const int c = wcnt[w][d];
-        lr[j] = c + before;
-        if (before == 0) wcnt[w][d] = c + __popcll(peers);
-      }
-    }
-    __syncthreads();
-    // Per digit (thread t < kOrdBins): per-wave exclusive offsets and the digit total; then the
-    // exclusive scan over digits gives each digit's start.
-    int tot = 0;
-    if (tid < kOrdBins) {
-#pragma unroll
-      for (int ww = 0; ww < kOrdWaves; ++ww) {
-        const int c = wcnt[ww][tid];
-        wcnt[ww][tid] = tot;
-        tot += c;
-      }
-    }
-    const int start = block_excl_scan_1024(tid < kOrdBins ? tot : 0, wsum);
-    if (tid < kOrdBins) run[tid] = start;
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < kOrdItems; ++j) {
-      const int e = wfirst + j * 64 + lane;
-      if (j < ipw && e < wlimit) {
-        const int d = (int)((kk[j] >> shift) & (uint32_t)mask);
-        const int pos = run[d] + wcnt[w][d] + lr[j];
-        skey[pos] = kk[j];
-        spos[pos] = pp[j];
-      }
-    }
-    __syncthreads();
+  for (int j = 0; j < kOrdItems; ++j) {
+    const int e = wfirst + j * 64 + lane;
+    const bool valid = e < wlimit;
+    kk[j] = valid ? ksrc[t0 + e] : 0u;
+    vv[j] = valid ? vsrc[t0 + e] : 0;
   }
-  for (int i = tid; i < size; i += kOrdThreads)
-    order[w0 + i] = perm ? perm[w0 + spos[i]] : (int32_t)(w0 + spos[i]);
+#pragma unroll
+  for (int j = 0; j < kOrdItems; ++j) {
+    lr[j] = 0;
+    if (j >= ipw) continue;  // uniform
+    const bool valid = wfirst + j * 64 + lane < wlimit;
+    const int d = (int)((kk[j] >> shift) & (uint32_t)mask);
+    uint64_t peers = __ballot(valid);
+    for (int b = 0; b < dbits; ++b) {
+      const bool bit = (d >> b) & 1;
+      const uint64_t mb = __ballot(valid && bit);
+      peers &= bit ? mb : ~mb;
+    }
+    if (valid) {
+      const int before = __popcll(peers & lt_mask);
+      const int c = wcnt[w][d];
+      lr[j] = c + before;
+      if (before == 0) wcnt[w][d] = c + __popcll(peers);
+    }
+  }
+  __syncthreads();
+  if (tid < kOrdBins) {  // per digit: exclusive offsets of the waves
+    int run = 0;
+#pragma unroll
+    for (int ww = 0; ww < kOrdWaves; ++ww) {
+      const int c = wcnt[ww][tid];
+      wcnt[ww][tid] = run;
+      run += c;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < kOrdItems; ++j) {
+    const int e = wfirst + j * 64 + lane;
+    if (j < ipw && e < wlimit) {
+      const int d = (int)((kk[j] >> shift) & (uint32_t)mask);
+      const int64_t pos = win0 + start[d] + wcnt[w][d] + lr[j];
+      if (kdst) kdst[pos] = kk[j];
+      vdst[pos] = vv[j];
+    }
+  }
 }
 
 }  // namespace
@@ -142,9 +203,37 @@ __global__ void __launch_bounds__(kOrdThreads)
 int conv_order_launch(tsc_ctx* ctx, const int32_t* nbr, const int32_t* perm, int64_t N,
                       int32_t* order) {
   if (N == 0) return TSC_OK;
+  const int ntiles = (int)((N + kOrdTile - 1) / kOrdTile);
+  const int nwin = (ntiles + kOrdTilesPerWin - 1) / kOrdTilesPerWin;
+  const size_t need = 2 * align_up((size_t)N * 4, 256) + 2 * align_up((size_t)N * 4, 256) +
+                      2 * align_up((size_t)ntiles * kOrdBins * 4, 256);
+  void* ws;
+  int st = workspace(ctx, need, &ws);
+  if (st) return st;
+  Carve cv(ws);
+  uint32_t* kA = cv.take<uint32_t>(N);
+  uint32_t* kB = cv.take<uint32_t>(N);
+  int32_t* vA = cv.take<int32_t>(N);
+  int32_t* vB = cv.take<int32_t>(N);
+  int* counts = cv.take<int>((int64_t)ntiles * kOrdBins);
+  int* offs = cv.take<int>((int64_t)ntiles * kOrdBins);
+  hipStream_t s = ctx->stream;
   ProfScope p(ctx, "conv_order");
-  const unsigned grid = (unsigned)((N + kOrdWin - 1) / kOrdWin);
-  conv_order_kernel<<<grid, kOrdThreads, 0, ctx->stream>>>(nbr, perm, N, order);
+  ord_mask_kernel<<<ntiles, kOrdThreads, 0, s>>>(nbr, perm, N, kA, vA, counts);
+  uint32_t *kc = kA, *kn = kB;
+  int32_t *vc = vA, *vn = vB;
+  for (int pass = 0; pass < kOrdPasses; ++pass) {
+    const int shift = pass * kOrdDigitBits;
+    const int dbits = kOrdMaskBits - shift < kOrdDigitBits ? kOrdMaskBits - shift : kOrdDigitBits;
+    const bool last = pass == kOrdPasses - 1;
+    if (pass > 0) ord_hist_kernel<<<ntiles, kOrdThreads, 0, s>>>(kc, N, shift, counts);
+    ord_scan_kernel<<<nwin, kOrdBins, 0, s>>>(counts, ntiles, offs);
+    ord_scatter_kernel<<<ntiles, kOrdThreads, 0, s>>>(kc, vc, N, shift, dbits, offs,
+                                                      last ? nullptr : kn,
+                                                      last ? order : vn);
+    std::swap(kc, kn);
+    std::swap(vc, vn);
+  }
   return check_hip(hipGetLastError(), "conv_order launch");
 }
 
