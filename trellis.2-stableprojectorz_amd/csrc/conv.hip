@@ -130,15 +130,18 @@ __device__ __forceinline__ void wait_vmcnt() {
 // Block -> (row tile, column tile).  The hardware hands block b to XCD b % 8, and each XCD has
 // its own L2.  When the column tiles divide 8, each XCD owns one column tile -- its slice of the
 // weights stays resident in that XCD's L2 -- and a contiguous range of row tiles (rows in
-// spatial order, so gathered neighbor rows are reused there too).  Otherwise each XCD gets a
-// contiguous run of (row, column) tiles with the column tiles of one row tile adjacent.
+// spatial order, so gathered neighbor rows are reused there too), dealt from the end of the
+// range: in the conv row order the late tiles of each sort window use more taps (20.5 vs 23.4 on
+// average, first vs last quarter, on a 512-channel 2-voxel shell), and starting the longer
+// tiles first shortens the tail of the launch (2-3 % measured).  Otherwise each XCD
+// gets a contiguous run of (row, column) tiles with the column tiles of one row tile adjacent.
 // per_xcd = blocks per XCD (grid = 8 * per_xcd), computed by tile_grid() on the host.
 __device__ __forceinline__ bool tile_of(int bid, int m_tiles, int n_tiles, int per_xcd,
                                         int* m_tile, int* n_tile) {
   const int xcd = bid & 7, i = bid >> 3;
   if (8 % n_tiles == 0) {
     *n_tile = xcd % n_tiles;
-    *m_tile = (xcd / n_tiles) * per_xcd + i;
+    *m_tile = (xcd / n_tiles) * per_xcd + (per_xcd - 1 - i);
     return *m_tile < m_tiles;
   }
   const int logical = xcd * per_xcd + i;

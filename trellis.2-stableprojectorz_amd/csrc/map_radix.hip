@@ -317,8 +317,8 @@ __global__ void __launch_bounds__(RT)
                        int lb, int64_t cells, int64_t Z, int64_t ncol, int64_t n,
                        int32_t* __restrict__ col_start) {
   // smem: the key bitmap, or the LSD digit counters run[LNB] + wcnt[WAVES][LNB].
-  __shared__ uint32_t smem[kBitmapWords];
-  __shared__ uint16_t wpre[kBitmapWords];  // set bits in the words before each word
+  __shared__ __attribute__((aligned(16))) uint32_t smem[kBitmapWords];
+  __shared__ __attribute__((aligned(16))) uint16_t wpre[kBitmapWords];  // set bits before each word
   __shared__ int wsum[WAVES];
   static_assert(kBitmapWords >= LNB * (WAVES + 1), "LSD counters alias the bitmap");
   static_assert(RTILE <= 65535, "prefix counts fit 16 bits");
@@ -361,31 +361,103 @@ __global__ void __launch_bounds__(RT)
     }
     dup = __syncthreads_or(dup);
     if (!dup) {
-      // Per-word prefix counts: thread t owns words [t*wpt, (t+1)*wpt).
+      // Per-word prefix counts: thread t owns words [t*wpt, (t+1)*wpt), one block scan of the
+      // per-thread totals.  At the full bitmap (16 words per thread) the words are read and the
+      // 16-bit prefixes written as 16-byte vectors.
       const int wpt = (nwords + RT - 1) / RT;
-      int sum = 0;
-      for (int q = 0; q < wpt; ++q) {
-        const int wi = tid * wpt + q;
-        if (wi < nwords) sum += __popc(bits[wi]);
+      constexpr int kWpt = kBitmapWords / RT;
+      int cw[kWpt];
+      if (wpt == kWpt) {
+        const uint4* bv = (const uint4*)bits + tid * (kWpt / 4);
+#pragma unroll
+        for (int q = 0; q < kWpt / 4; ++q) {
+          const uint4 x = bv[q];
+          cw[4 * q] = __popc(x.x);
+          cw[4 * q + 1] = __popc(x.y);
+          cw[4 * q + 2] = __popc(x.z);
+          cw[4 * q + 3] = __popc(x.w);
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < kWpt; ++q) {
+          const int wi = tid * wpt + q;
+          cw[q] = (q < wpt && wi < nwords) ? __popc(bits[wi]) : 0;
+        }
       }
+      int sum = 0;
+#pragma unroll
+      for (int q = 0; q < kWpt; ++q) sum += cw[q];
       int tot;
       int pre = block_excl_scan(sum, wsum, &tot);
-      for (int q = 0; q < wpt; ++q) {
-        const int wi = tid * wpt + q;
-        if (wi < nwords) {
-          wpre[wi] = (uint16_t)pre;
-          pre += __popc(bits[wi]);
+      if (wpt == kWpt) {
+        uint32_t pk[kWpt / 2];
+#pragma unroll
+        for (int q = 0; q < kWpt / 2; ++q) {
+          const uint32_t lo = (uint32_t)pre;
+          pre += cw[2 * q];
+          pk[q] = lo | ((uint32_t)pre << 16);
+          pre += cw[2 * q + 1];
+        }
+        uint4* wp = (uint4*)wpre + tid * (kWpt / 8);
+#pragma unroll
+        for (int q = 0; q < kWpt / 8; ++q)
+          wp[q] = make_uint4(pk[4 * q], pk[4 * q + 1], pk[4 * q + 2], pk[4 * q + 3]);
+      } else {
+#pragma unroll
+        for (int q = 0; q < kWpt; ++q) {
+          const int wi = tid * wpt + q;
+          if (q < wpt && wi < nwords) {
+            wpre[wi] = (uint16_t)pre;
+            pre += cw[q];
+          }
         }
       }
       __syncthreads();
+      int rk[RI];
 #pragma unroll
       for (int j = 0; j < RI; ++j) {
         const int i = j * RT + tid;
         if (i < size) {
           const int wi = loc[j] >> 5;
-          const int r = wpre[wi] + __popc(bits[wi] & ((1u << (loc[j] & 31)) - 1u));
-          kout[start + r] = kk[j];
-          vout[start + r] = vv[j];
+          rk[j] = wpre[wi] + __popc(bits[wi] & ((1u << (loc[j] & 31)) - 1u));
+        }
+      }
+      // Column starts from the bitmap, before the staging below overwrites it: columns whose
+      // first key c*Z lies in this bucket's key range [b << lb, (b+1) << lb).
+      if (col_start) {
+        const int64_t key_lo = (int64_t)b << lb;
+        const int64_t key_hi = std::min<int64_t>((int64_t)(b + 1) << lb, cells);
+        const int64_t c_lo = (key_lo + Z - 1) / Z, c_hi = (key_hi + Z - 1) / Z;
+        for (int64_t c = c_lo + tid; c < c_hi; c += RT) {
+          const int local = (int)(c * Z - key_lo);
+          const int wi = local >> 5;
+          col_start[c] = (int32_t)(start + wpre[wi] + __popc(bits[wi] & ((1u << (local & 31)) - 1u)));
+        }
+      }
+      if constexpr (sizeof(K) == 4) {
+        // Stage keys, then rows, in sorted order through LDS (the bitmap is no longer needed)
+        // so that the global writes are coalesced runs instead of one cache line per element.
+        int32_t* st = (int32_t*)smem;
+        static_assert(kBitmapWords >= RTILE, "staging holds a full bucket");
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < RI; ++j)
+          if (j * RT + tid < size) st[rk[j]] = (int32_t)kk[j];
+        __syncthreads();
+        for (int i = tid; i < size; i += RT) kout[start + i] = (K)st[i];
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < RI; ++j)
+          if (j * RT + tid < size) st[rk[j]] = vv[j];
+        __syncthreads();
+        for (int i = tid; i < size; i += RT) vout[start + i] = st[i];
+      } else {
+#pragma unroll
+        for (int j = 0; j < RI; ++j) {
+          if (j * RT + tid < size) {
+            kout[start + rk[j]] = kk[j];
+            vout[start + rk[j]] = vv[j];
+          }
         }
       }
       by_bitmap = true;
@@ -453,23 +525,15 @@ __global__ void __launch_bounds__(RT)
     }
   }
   if (!col_start) return;
+  if (b == nbk - 1 && tid == 0) col_start[ncol] = (int32_t)n;
+  if (by_bitmap) return;
   __syncthreads();
   // Columns whose first key c*Z lies in this bucket's key range [b << lb, (b+1) << lb).
   const int64_t key_lo = (int64_t)b << lb;
   const int64_t key_hi = std::min<int64_t>((int64_t)(b + 1) << lb, cells);
   const int64_t c_lo = (key_lo + Z - 1) / Z, c_hi = (key_hi + Z - 1) / Z;
-  for (int64_t c = c_lo + tid; c < c_hi; c += RT) {
-    int64_t pos;
-    if (by_bitmap) {
-      const int local = (int)(c * Z - key_lo);
-      const int wi = local >> 5;
-      pos = wpre[wi] + __popc(bits[wi] & ((1u << (local & 31)) - 1u));
-    } else {
-      pos = lower_bound<K>(kout + start, 0, size, (K)(c * Z));
-    }
-    col_start[c] = (int32_t)(start + pos);
-  }
-  if (b == nbk - 1 && tid == 0) col_start[ncol] = (int32_t)n;
+  for (int64_t c = c_lo + tid; c < c_hi; c += RT)
+    col_start[c] = (int32_t)(start + lower_bound<K>(kout + start, 0, size, (K)(c * Z)));
 }
 
 // Column-index probe for the column-parallel fill: the neighbor column's keys occupy
