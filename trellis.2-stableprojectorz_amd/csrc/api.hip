@@ -28,30 +28,42 @@ int check_hip(hipError_t e, const char* what) {
   return fail(TSC_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
-int workspace(tsc_ctx* ctx, size_t bytes, void** out) {
-  if (bytes <= ctx->ws_bytes) {
-    *out = ctx->ws;
+namespace {
+// Grows a stream-ordered device buffer to at least `bytes` (with 25 % headroom, at least 1 MiB).
+int grow_buffer(tsc_ctx* ctx, void** buf, size_t* cap, size_t bytes, const char* what,
+                void** out) {
+  if (bytes <= *cap) {
+    *out = *buf;
     return TSC_OK;
   }
   // Growing: earlier enqueued work may still use the old block.
   int st = check_hip(hipStreamSynchronize(ctx->stream), "workspace sync");
   if (st) return st;
-  if (ctx->ws) {
-    st = check_hip(hipFree(ctx->ws), "workspace free");
-    ctx->ws = nullptr;
-    ctx->ws_bytes = 0;
+  if (*buf) {
+    st = check_hip(hipFree(*buf), "workspace free");
+    *buf = nullptr;
+    *cap = 0;
     if (st) return st;
   }
   size_t want = std::max(bytes + bytes / 4, (size_t)(1u << 20));
   void* p = nullptr;
   if (hipMalloc(&p, want) != hipSuccess) {
     (void)hipGetLastError();
-    return fail(TSC_ERR_OOM, "workspace: cannot allocate %zu bytes", want);
+    return fail(TSC_ERR_OOM, "%s: cannot allocate %zu bytes", what, want);
   }
-  ctx->ws = p;
-  ctx->ws_bytes = want;
+  *buf = p;
+  *cap = want;
   *out = p;
   return TSC_OK;
+}
+}  // namespace
+
+int workspace(tsc_ctx* ctx, size_t bytes, void** out) {
+  return grow_buffer(ctx, &ctx->ws, &ctx->ws_bytes, bytes, "workspace", out);
+}
+
+int sched_workspace(tsc_ctx* ctx, size_t bytes, void** out) {
+  return grow_buffer(ctx, &ctx->ws_sched, &ctx->ws_sched_bytes, bytes, "schedule workspace", out);
 }
 
 void prof_clear(tsc_ctx* ctx) {
@@ -149,6 +161,7 @@ int tsc_ctx_destroy(tsc_ctx* ctx) {
   DeviceGuard g(ctx->device);
   int st = check_hip(hipStreamSynchronize(ctx->stream), "ctx_destroy sync");
   if (ctx->ws) (void)hipFree(ctx->ws);
+  if (ctx->ws_sched) (void)hipFree(ctx->ws_sched);
   prof_clear(ctx);
   delete ctx;
   return st;

@@ -75,8 +75,6 @@ __device__ __forceinline__ int swz(int row, int part) {
   return part ^ ((row / rows_per_256) % PPR);
 }
 
-constexpr int kTaps = 27;
-
 // Zeros in device memory: the source of the gathered A pieces whose neighbor is absent (a
 // direct-to-LDS load cannot be told to write zeros).  Rows of up to kZeroBytes bytes: a zero
 // piece advances through it by the same Ci offset as a real feature row.
@@ -129,18 +127,24 @@ __device__ __forceinline__ void wait_vmcnt() {
 
 // Block -> (row tile, column tile).  The hardware hands block b to XCD b % 8, and each XCD has
 // its own L2.  When the column tiles divide 8, each XCD owns one column tile -- its slice of the
-// weights stays resident in that XCD's L2 -- and a contiguous range of row tiles (rows in
-// spatial order, so gathered neighbor rows are reused there too), dealt from the end of the
-// range: in the conv row order the late tiles of each sort window use more taps (20.5 vs 23.4 on
-// average, first vs last quarter, on a 512-channel 2-voxel shell), and starting the longer
-// tiles first shortens the tail of the launch (2-3 % measured).  Otherwise each XCD
-// gets a contiguous run of (row, column) tiles with the column tiles of one row tile adjacent.
-// per_xcd = blocks per XCD (grid = 8 * per_xcd), computed by tile_grid() on the host.
+// weights stays resident in that XCD's L2 -- and the XCDs of one column tile form a group that
+// shares its row tiles:
+//   * with a schedule (tile_map, built by tile_schedule_kernel): the XCD's i-th block takes slot
+//     i of its group's list, which holds the group's row tiles longest first (-1: no tile);
+//   * without: a contiguous range of row tiles, dealt from the end of the range (in the conv row
+//     order the late tiles of each sort window use more taps).
+// Otherwise each XCD gets a contiguous run of (row, column) tiles with the column tiles of one
+// row tile adjacent.  per_xcd = blocks per XCD (grid = 8 * per_xcd), from tile_grid_per_xcd().
 __device__ __forceinline__ bool tile_of(int bid, int m_tiles, int n_tiles, int per_xcd,
-                                        int* m_tile, int* n_tile) {
+                                        const int32_t* tile_map, int* m_tile, int* n_tile) {
   const int xcd = bid & 7, i = bid >> 3;
   if (8 % n_tiles == 0) {
     *n_tile = xcd % n_tiles;
+    const int slot = (xcd / n_tiles) * per_xcd + i;
+    if (tile_map) {
+      *m_tile = tile_map[slot];
+      return *m_tile >= 0;
+    }
     *m_tile = (xcd / n_tiles) * per_xcd + (per_xcd - 1 - i);
     return *m_tile < m_tiles;
   }
@@ -156,6 +160,72 @@ inline int32_t tile_grid_per_xcd(int32_t m_tiles, int32_t n_tiles) {
     return (m_tiles + groups - 1) / groups;
   }
   return (int32_t)(((int64_t)m_tiles * n_tiles + 7) / 8);
+}
+
+constexpr int kTaps = 27;
+
+// Longest-first tile schedule.  A row tile's running time is about proportional to the taps it
+// uses (the OR of its rows' neighbor masks); with a few rounds of tiles per CU, dealing them in
+// row order leaves CUs idle at the end of the launch.  tile_cost_kernel counts each tile's taps;
+// tile_schedule_kernel ranks the tiles by decreasing count (counting sort, ties in any order) and
+// deals rank k to group g = k mod G on even rounds r = k / G and to G-1 - (k mod G) on odd ones
+// (a serpentine), slot g*per + r.  Every group gets a near-equal share of the work, and each
+// group's blocks start with its longest tiles.  Slots past the tile count get -1.  The schedule
+// only decides which block computes which tile: every tile's arithmetic is unchanged.
+constexpr int kSchedThreads = 256;
+constexpr int kSchedMaxTiles = 1 << 16;
+
+__global__ void __launch_bounds__(kSchedThreads)
+    tile_cost_kernel(const int32_t* __restrict__ nbr, const int32_t* __restrict__ order, int64_t N,
+                     int bm, int32_t* __restrict__ cost) {
+  __shared__ int32_t sRow[256];
+  __shared__ uint32_t sMask;
+  const int tid = threadIdx.x;
+  const int64_t m0 = (int64_t)blockIdx.x * bm;
+  if (tid == 0) sMask = 0u;
+  for (int r = tid; r < bm; r += kSchedThreads) {
+    const int64_t pos = m0 + r;
+    sRow[r] = pos < N ? (order ? order[pos] : (int32_t)pos) : -1;
+  }
+  __syncthreads();
+  uint32_t mask = 0u;
+  for (int j = tid; j < bm * kTaps; j += kSchedThreads) {
+    const int r = j / kTaps, v = j - r * kTaps;
+    const int32_t row = sRow[r];
+    if (row >= 0 && nbr[(int64_t)row * kTaps + v] >= 0) mask |= 1u << v;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mask |= __shfl_xor(mask, off, 64);
+  if ((tid & 63) == 0 && mask) atomicOr(&sMask, mask);
+  __syncthreads();
+  if (tid == 0) cost[blockIdx.x] = __popc(sMask);
+}
+
+__global__ void __launch_bounds__(kSchedThreads)
+    tile_schedule_kernel(const int32_t* __restrict__ cost, int32_t m_tiles, int32_t groups,
+                         int32_t per, int32_t* __restrict__ tile_map) {
+  __shared__ int hist[kTaps + 1];
+  __shared__ int next[kTaps + 1];
+  const int tid = threadIdx.x;
+  if (tid <= kTaps) hist[tid] = 0;
+  __syncthreads();
+  for (int t = tid; t < m_tiles; t += kSchedThreads) atomicAdd(&hist[cost[t]], 1);
+  __syncthreads();
+  if (tid == 0) {
+    int run = 0;
+    for (int c = kTaps; c >= 0; --c) {
+      next[c] = run;
+      run += hist[c];
+    }
+  }
+  __syncthreads();
+  auto slot_of = [&](int k) {
+    const int r = k / groups, q = k - r * groups;
+    const int g = (r & 1) ? groups - 1 - q : q;
+    return g * per + r;
+  };
+  for (int t = tid; t < m_tiles; t += kSchedThreads) tile_map[slot_of(atomicAdd(&next[cost[t]], 1))] = t;
+  for (int k = m_tiles + tid; k < groups * per; k += kSchedThreads) tile_map[slot_of(k)] = -1;
 }
 
 template <typename T, int BM, int BN, int KB, int STAGES, int WM, int WN>
@@ -208,8 +278,8 @@ __global__ void __launch_bounds__(64 * WM * WN)
     conv_mfma_kernel(const T* __restrict__ feats, const T* __restrict__ weight,
                      const T* __restrict__ bias, const int32_t* __restrict__ nbr,
                      const int32_t* __restrict__ order, int64_t N, int32_t Ci, int32_t Co,
-                     int32_t m_tiles, int32_t n_tiles, int32_t per_xcd, const T* residual,
-                     T* out) {
+                     int32_t m_tiles, int32_t n_tiles, int32_t per_xcd,
+                     const int32_t* __restrict__ tile_map, const T* residual, T* out) {
   using C = ConvCfg<T, BM, BN, KB, STAGES, WM, WN>;
   constexpr int SB = C::STAGE_BYTES;
   __shared__ __attribute__((aligned(16))) unsigned char r0[SB];
@@ -227,7 +297,7 @@ __global__ void __launch_bounds__(64 * WM * WN)
   unsigned char* const ring[8] = {r0, r1, r2, r3, r4, r5, r6, r7};
 
   int m_tile, n_tile;
-  if (!tile_of(blockIdx.x, m_tiles, n_tiles, per_xcd, &m_tile, &n_tile)) return;
+  if (!tile_of(blockIdx.x, m_tiles, n_tiles, per_xcd, tile_map, &m_tile, &n_tile)) return;
   const int64_t m0 = (int64_t)m_tile * BM;
   const int n0 = n_tile * BN;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -449,7 +519,7 @@ __global__ void __launch_bounds__(64 * WM * WN)
   __shared__ uint32_t sMask;
 
   int m_tile, n_tile;
-  if (!tile_of(blockIdx.x, m_tiles, n_tiles, per_xcd, &m_tile, &n_tile)) return;
+  if (!tile_of(blockIdx.x, m_tiles, n_tiles, per_xcd, nullptr, &m_tile, &n_tile)) return;
   const int64_t m0 = (int64_t)m_tile * BM;
   const int n0 = n_tile * BN;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -623,6 +693,25 @@ int launch_cfg(tsc_ctx* ctx, const ConvArgs& a) {
   const int32_t n_tiles = a.Co / BN;
   const int32_t per_xcd = tile_grid_per_xcd(m_tiles, n_tiles);
   const unsigned grid = (unsigned)per_xcd * 8u;
+  // Longest-first schedule for the 256-row tile (several rounds of long tiles per CU).
+  const int32_t* tile_map = nullptr;
+  if (BM == 256 && 8 % n_tiles == 0 && m_tiles <= kSchedMaxTiles) {
+    const int32_t groups = 8 / n_tiles;
+    void* ws;
+    int st = sched_workspace(ctx, ((size_t)m_tiles + (size_t)groups * per_xcd) * 4, &ws);
+    if (st) return st;
+    int32_t* cost = (int32_t*)ws;
+    int32_t* map = cost + m_tiles;
+    {
+      ProfScope p(ctx, "conv_tile_cost");
+      tile_cost_kernel<<<m_tiles, kSchedThreads, 0, ctx->stream>>>(a.nbr, a.order, a.N, BM, cost);
+    }
+    {
+      ProfScope p(ctx, "conv_tile_schedule");
+      tile_schedule_kernel<<<1, kSchedThreads, 0, ctx->stream>>>(cost, m_tiles, groups, per_xcd, map);
+    }
+    tile_map = map;
+  }
   static const std::string name = std::string("conv_") +
       (sizeof(T) == 4 ? "f32" : std::is_same<T, __bf16>::value ? "bf16" : "f16") + "_" +
       std::to_string(BM) + "x" + std::to_string(BN) + "_k" + std::to_string(KB) + "_s" +
@@ -630,7 +719,7 @@ int launch_cfg(tsc_ctx* ctx, const ConvArgs& a) {
   ProfScope p(ctx, name.c_str());
   conv_mfma_kernel<T, BM, BN, KB, STAGES, WM, WN, EPI><<<grid, 64 * WM * WN, 0, ctx->stream>>>(
       (const T*)a.feats, (const T*)a.weight, (const T*)a.bias, a.nbr, a.order, a.N, a.Ci, a.Co,
-      m_tiles, n_tiles, per_xcd, (const T*)a.residual, (T*)a.out);
+      m_tiles, n_tiles, per_xcd, tile_map, (const T*)a.residual, (T*)a.out);
   return check_hip(hipGetLastError(), "conv launch");
 }
 

@@ -27,6 +27,10 @@ struct tsc_ctx {
   // Growable device workspace (stream-ordered users; grown only after a stream sync).
   void* ws = nullptr;
   size_t ws_bytes = 0;
+  // Second growable buffer for the conv tile schedule (a conv may run while `ws` holds the
+  // intermediate rows of a ResBlock).
+  void* ws_sched = nullptr;
+  size_t ws_sched_bytes = 0;
   bool profile = false;
   std::vector<tsc_prof_rec> prof;      // pending launches
   std::vector<tsc_prof_agg> prof_agg;  // aggregated by tsc_profile_collect
@@ -40,6 +44,8 @@ int check_hip(hipError_t e, const char* what);
 
 // Ensures ctx->ws holds at least `bytes`; returns TSC_OK or an error status.
 int workspace(tsc_ctx* ctx, size_t bytes, void** out);
+// The same for ctx->ws_sched.
+int sched_workspace(tsc_ctx* ctx, size_t bytes, void** out);
 
 void prof_clear(tsc_ctx* ctx);
 
