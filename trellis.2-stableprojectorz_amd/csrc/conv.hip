@@ -791,20 +791,32 @@ __global__ void __launch_bounds__(NT)
   const int stride = (int)(gridDim.x >> 3) * NW;
   // Tiles are software-pipelined: while tile t computes, the neighbor indices of tile t+1 and
   // the row numbers of tile t+2 are in flight, so a tile starts without a dependent round trip.
-  // Neighbor indices: iteration it reads rows 2*it and 2*it+1 with lanes 0-26 and 27-53 on
-  // consecutive words of each 108-byte row; they land in the wave's LDS slice as [row][tap]
-  // (odd row stride: the slot fills' 16-lane reads of one tap hit distinct banks).
-  const int lv = lane % kTaps, lr = lane / kTaps;  // lr = 2 for the idle lanes 54-63
+  // Neighbor indices: iteration it reads rows 7*it .. 7*it+6, lane l < 63 taking taps
+  // 3*(l%9) .. 3*(l%9)+2 of row 7*it + l/9 as one 12-byte load (five load instructions per tile;
+  // the address unit's work per gather-heavy tile is what bounds this kernel).  They land in the
+  // wave's LDS slice as [row][tap]: lane l writes words 3l .. 3l+2 of the 7-row block, stride 3
+  // across lanes, conflict-free (odd row stride: the slot fills' 16-lane reads of one tap hit
+  // distinct banks).
+  constexpr int kNbrIters = (32 + 6) / 7;
+  const int nr = lane / 9, nk = lane - nr * 9;  // nr = 7 for the idle lane 63
   auto load_row = [&](int t) -> int32_t {
     const int64_t pos = (int64_t)t * 32 + (lane & 31);
     return (t < t_end && pos < N) ? (order ? order[pos] : (int32_t)pos) : -1;
   };
-  int32_t val[16];
+  int32_t val[kNbrIters][3];
   auto load_nbr = [&](int32_t rows) {
 #pragma unroll
-    for (int it = 0; it < 16; ++it) {
-      const int32_t row = __shfl(rows, (2 * it + lr) & 31, 64);
-      val[it] = (lr < 2 && row >= 0) ? nbr[(int64_t)row * kTaps + lv] : -1;
+    for (int it = 0; it < kNbrIters; ++it) {
+      const int rr = it * 7 + nr;
+      const int32_t row = __shfl(rows, rr & 31, 64);
+      if (nr < 7 && rr < 32 && row >= 0) {
+        const int32_t* src = nbr + (int64_t)row * kTaps + 3 * nk;
+        val[it][0] = src[0];
+        val[it][1] = src[1];
+        val[it][2] = src[2];
+      } else {
+        val[it][0] = val[it][1] = val[it][2] = -1;
+      }
     }
   };
   int tile = t_begin + (int)(blockIdx.x >> 3) * NW + wid;
@@ -813,8 +825,14 @@ __global__ void __launch_bounds__(NT)
   load_nbr(my_row);
   for (; tile < t_end; tile += stride) {
 #pragma unroll
-    for (int it = 0; it < 16; ++it)
-      if (lr < 2) nbw[(2 * it + lr) * kTaps + lv] = val[it];
+    for (int it = 0; it < kNbrIters; ++it) {
+      if (nr < 7 && it * 7 + nr < 32) {
+        int32_t* dst = nbw + (it * 7 + nr) * kTaps + 3 * nk;
+        dst[0] = val[it][0];
+        dst[1] = val[it][1];
+        dst[2] = val[it][2];
+      }
+    }
     load_nbr(row_next);
     const int32_t row_after = load_row(tile + 2 * stride);
     // Tap mask: lane l < 54 ORs tap l % 27 over rows [16*(l/27), 16*(l/27)+16).
