@@ -178,21 +178,20 @@ constexpr int kSchedMaxTiles = 1 << 16;
 __global__ void __launch_bounds__(kSchedThreads)
     tile_cost_kernel(const int32_t* __restrict__ nbr, const int32_t* __restrict__ order, int64_t N,
                      int bm, int32_t* __restrict__ cost) {
-  __shared__ int32_t sRow[256];
   __shared__ uint32_t sMask;
   const int tid = threadIdx.x;
   const int64_t m0 = (int64_t)blockIdx.x * bm;
   if (tid == 0) sMask = 0u;
-  for (int r = tid; r < bm; r += kSchedThreads) {
-    const int64_t pos = m0 + r;
-    sRow[r] = pos < N ? (order ? order[pos] : (int32_t)pos) : -1;
-  }
   __syncthreads();
   uint32_t mask = 0u;
-  for (int j = tid; j < bm * kTaps; j += kSchedThreads) {
-    const int r = j / kTaps, v = j - r * kTaps;
-    const int32_t row = sRow[r];
-    if (row >= 0 && nbr[(int64_t)row * kTaps + v] >= 0) mask |= 1u << v;
+  for (int r = tid; r < bm; r += kSchedThreads) {  // one 108-byte neighbor row per thread
+    const int64_t pos = m0 + r;
+    const int32_t row = pos < N ? (order ? order[pos] : (int32_t)pos) : -1;
+    if (row >= 0) {
+      const int32_t* nr = nbr + (int64_t)row * kTaps;
+#pragma unroll
+      for (int v = 0; v < kTaps; ++v) mask |= (uint32_t)(nr[v] >= 0) << v;
+    }
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) mask |= __shfl_xor(mask, off, 64);
