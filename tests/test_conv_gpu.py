@@ -89,6 +89,29 @@ def test_conv_dtypes_and_shapes(pkg, dev, dtype, ci, co):
         assert err <= TOL[dtype], err
 
 
+@pytest.mark.parametrize("ci,co,rows", [(64, 768, None), (64, 256, 100), (128, 512, 2000)])
+def test_conv_wide_tile_schedule(pkg, dev, ci, co, rows):
+    """256x256 tiles go through the longest-first schedule: three column tiles per row tile,
+    fewer row tiles than XCDs (empty schedule slots), and a partial last tile."""
+    coords = pkg.workloads.make_coords("resblock64_bf16")
+    if rows is not None:
+        coords = coords[coords[:, 0] == 0][:rows]
+    n = len(coords)
+    batch = int(coords[:, 0].max()) + 1
+    print(f"  conv schedule N={n} {ci}->{co}", flush=True)
+    m = _map(pkg, dev, coords, batch, (64, 64, 64))
+    dt = torch.bfloat16
+    f, f64 = _rounded(pkg.workloads.features(n, ci, 4), dt, dev)
+    w, w64 = _rounded(pkg.workloads.conv_weight(co, ci, 5), dt, dev)
+    out = pkg.sparse_conv3d(f, w, None, m).float().cpu().numpy()
+    nbr = m.nbr.cpu().numpy()
+    sel = np.sort(np.random.default_rng(6).choice(n, min(n, 700), replace=False))
+    ref = oracle.conv(f64, w64, None, nbr[sel])
+    assert rel_err(out[sel], ref) <= TOL[dt]
+    again = pkg.sparse_conv3d(f, w, None, m.nbr, order=m.perm)
+    assert torch.equal(again.float().cpu(), torch.from_numpy(out))
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_conv_order_invariance_bit_exact(pkg, dev, dtype):
     coords = pkg.workloads.make_coords("conv64_f32")
