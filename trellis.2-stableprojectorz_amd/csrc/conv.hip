@@ -246,12 +246,6 @@ struct ConvCfg {
   static constexpr int PPW = PIECES / WAVES;          // pieces per wave per stage
   static constexpr int IPW = (PPW + 63) / 64;         // load instructions per wave per stage
   static constexpr int STAGE_BYTES = PIECES * 16;
-  static constexpr int LDE = BN * (int)sizeof(T) + 16;  // epilogue row stride (bytes, padded)
-  // Output rows staged per epilogue pass: a multiple of 32 (one MFMA block) that fits in one
-  // ring stage.
-  static constexpr int EPI_ROWS_FIT = STAGE_BYTES / LDE / 32 * 32;
-  static constexpr int EPI_ROWS = EPI_ROWS_FIT >= BM ? BM : EPI_ROWS_FIT;
-  static_assert(EPI_ROWS >= 32 && BM % EPI_ROWS == 0, "epilogue pass must hold 32-row blocks");
   static_assert(KB % 32 == 0 && KB <= 128, "chunk must be 32..128 bytes");
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32x32");
   static_assert(PIECES % WAVES == 0, "every wave issues the same loads");
@@ -447,10 +441,20 @@ __global__ void __launch_bounds__(64 * WM * WN)
   }
 
   // Epilogue: bias (+ residual) in fp32, one rounding, staged through ring stage 0 (free now) in
-  // passes of RPP rows for 16-byte stores of the scattered output rows.
+  // passes of RPP rows for 16-byte stores of the scattered output rows.  With a residual the
+  // staged values stay fp32 when 32 rows of them fit in a stage: the residual is then read in the
+  // same 16-byte runs as the output (one coalesced load per run instead of one 2-byte load per
+  // element), added, and rounded once.
   __syncthreads();
-  constexpr int RPP = C::EPI_ROWS;
-  constexpr int PIECES_PER_ROW = BN / C::EPP;
+  constexpr bool RES = EPI == TSC_EPI_BIAS_RESIDUAL;
+  constexpr bool RES_IN_COPY = RES && (sizeof(T) == 4 || SB / (BN * 4) >= 32);
+  using S = typename std::conditional<RES_IN_COPY, float, T>::type;  // staged element type
+  constexpr int ROWB = BN * (int)sizeof(S);
+  constexpr int LDE = SB / (ROWB + 16) >= 32 ? ROWB + 16 : ROWB;  // padded row stride if it fits
+  constexpr int RFIT = SB / LDE / 32 * 32;
+  constexpr int RPP = RFIT >= BM ? BM : RFIT;
+  static_assert(RPP >= 32 && BM % RPP == 0, "epilogue pass must hold 32-row blocks");
+  constexpr int PIECES_PER_ROW = BN / C::EPP;  // 16-byte output pieces per row
   unsigned char* sE = r0;
 #pragma unroll
   for (int p0 = 0; p0 < BM; p0 += RPP) {
@@ -466,11 +470,13 @@ __global__ void __launch_bounds__(64 * WM * WN)
         for (int e = 0; e < 16; ++e) {
           const int rl = rb + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
           float val = acc[i][j][e] + bv;
-          if (EPI == TSC_EPI_BIAS_RESIDUAL) {
+          if (RES && !RES_IN_COPY) {
             const int32_t row = sRow[rl];
             if (row >= 0) val += to_f32<T>(residual[(int64_t)row * Co + n0 + cl]);
           }
-          *(T*)(sE + (rl - p0) * C::LDE + cl * (int)sizeof(T)) = from_f32<T>(val);
+          S* dst = (S*)(sE + (rl - p0) * LDE + cl * (int)sizeof(S));
+          if constexpr (std::is_same<S, float>::value) *dst = val;
+          else *dst = from_f32<T>(val);
         }
       }
     }
@@ -478,9 +484,21 @@ __global__ void __launch_bounds__(64 * WM * WN)
     for (int q = tid; q < RPP * PIECES_PER_ROW; q += C::NT) {
       const int r = q / PIECES_PER_ROW, pc = q - r * PIECES_PER_ROW;
       const int32_t row = sRow[p0 + r];
-      if (row >= 0)
-        *(uint4*)(out + (int64_t)row * Co + n0 + pc * C::EPP) =
-            *(const uint4*)(sE + r * C::LDE + pc * 16);
+      if (row < 0) continue;
+      T* dst = out + (int64_t)row * Co + n0 + pc * C::EPP;
+      if constexpr (RES_IN_COPY) {
+        // The residual run is read before the output run is written by the same thread, so the
+        // output may alias the residual.
+        const uint4 rr = *(const uint4*)(residual + (int64_t)row * Co + n0 + pc * C::EPP);
+        const T* rt = (const T*)&rr;
+        const float* sv = (const float*)(sE + r * LDE + pc * C::EPP * 4);
+        T y[C::EPP];
+#pragma unroll
+        for (int k = 0; k < C::EPP; ++k) y[k] = from_f32<T>(sv[k] + to_f32<T>(rt[k]));
+        *(uint4*)dst = *(const uint4*)y;
+      } else {
+        *(uint4*)dst = *(const uint4*)(sE + r * LDE + pc * 16);
+      }
     }
     __syncthreads();
   }
