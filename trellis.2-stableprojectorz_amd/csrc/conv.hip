@@ -265,11 +265,12 @@ struct ConvCfg {
 //              for absent neighbors; K-contiguous weight rows for B), STAGES-1 chunks ahead.
 //              Every wave issues the same IPW loads per chunk, so "chunk c has landed" is the
 //              wave's own s_waitcnt vmcnt(IPW * chunks issued after c) followed by one
-//              s_barrier.  Each stage is a separate LDS array and the loop is unrolled by
-//              STAGES, so the compiler can see which stage a read touches and does not insert
-//              its own vmcnt(0) after the LDS-DMA loads.
+//              s_barrier.  All reads of the ring are inline asm, which the compiler's wait
+//              insertion does not treat as reads of the DMA target, so it adds no vmcnt(0)
+//              after the LDS-DMA loads.
 //   epilogue   fp32 accumulators + bias (+ residual) rounded once to T, staged through a padded
-//              LDS tile, written back as 16-byte runs of the scattered output rows.
+//              LDS tile (the whole ring), written back as 16-byte runs of the scattered output
+//              rows.
 template <typename T, int BM, int BN, int KB, int STAGES, int WM, int WN, int EPI>
 __global__ void __launch_bounds__(64 * WM * WN)
     conv_mfma_kernel(const T* __restrict__ feats, const T* __restrict__ weight,
@@ -279,19 +280,14 @@ __global__ void __launch_bounds__(64 * WM * WN)
                      const int32_t* __restrict__ tile_map, const T* residual, T* out) {
   using C = ConvCfg<T, BM, BN, KB, STAGES, WM, WN>;
   constexpr int SB = C::STAGE_BYTES;
-  __shared__ __attribute__((aligned(16))) unsigned char r0[SB];
-  __shared__ __attribute__((aligned(16))) unsigned char r1[SB];
-  __shared__ __attribute__((aligned(16))) unsigned char r2[STAGES > 2 ? SB : 16];
-  __shared__ __attribute__((aligned(16))) unsigned char r3[STAGES > 3 ? SB : 16];
-  __shared__ __attribute__((aligned(16))) unsigned char r4[STAGES > 4 ? SB : 16];
-  __shared__ __attribute__((aligned(16))) unsigned char r5[STAGES > 5 ? SB : 16];
-  __shared__ __attribute__((aligned(16))) unsigned char r6[STAGES > 6 ? SB : 16];
-  __shared__ __attribute__((aligned(16))) unsigned char r7[STAGES > 7 ? SB : 16];
+  __shared__ __attribute__((aligned(16))) unsigned char ring_mem[STAGES * SB];
   __shared__ int32_t sNbr[BM * kTaps];
   __shared__ int32_t sRow[BM];
   __shared__ int32_t sTaps[kTaps];
   __shared__ uint32_t sMask;
-  unsigned char* const ring[8] = {r0, r1, r2, r3, r4, r5, r6, r7};
+  unsigned char* ring[STAGES];
+#pragma unroll
+  for (int s = 0; s < STAGES; ++s) ring[s] = ring_mem + s * SB;
 
   int m_tile, n_tile;
   if (!tile_of(blockIdx.x, m_tiles, n_tiles, per_xcd, tile_map, &m_tile, &n_tile)) return;
@@ -440,22 +436,24 @@ __global__ void __launch_bounds__(64 * WM * WN)
     }
   }
 
-  // Epilogue: bias (+ residual) in fp32, one rounding, staged through ring stage 0 (free now) in
+  // Epilogue: bias (+ residual) in fp32, one rounding, staged through the ring (free now) in
   // passes of RPP rows for 16-byte stores of the scattered output rows.  With a residual the
-  // staged values stay fp32 when 32 rows of them fit in a stage: the residual is then read in the
-  // same 16-byte runs as the output (one coalesced load per run instead of one 2-byte load per
+  // staged values stay fp32 when 32 rows of them fit: the residual is then read in the same
+  // 16-byte runs as the output (one coalesced load per run instead of one 2-byte load per
   // element), added, and rounded once.
   __syncthreads();
+  constexpr int EB = STAGES * SB;  // staging bytes
   constexpr bool RES = EPI == TSC_EPI_BIAS_RESIDUAL;
-  constexpr bool RES_IN_COPY = RES && (sizeof(T) == 4 || SB / (BN * 4) >= 32);
+  constexpr bool RES_IN_COPY = RES && (sizeof(T) == 4 || EB / (BN * 4) >= 32);
   using S = typename std::conditional<RES_IN_COPY, float, T>::type;  // staged element type
   constexpr int ROWB = BN * (int)sizeof(S);
-  constexpr int LDE = SB / (ROWB + 16) >= 32 ? ROWB + 16 : ROWB;  // padded row stride if it fits
-  constexpr int RFIT = SB / LDE / 32 * 32;
-  constexpr int RPP = RFIT >= BM ? BM : RFIT;
-  static_assert(RPP >= 32 && BM % RPP == 0, "epilogue pass must hold 32-row blocks");
+  constexpr int LDE = EB / (ROWB + 16) >= 32 ? ROWB + 16 : ROWB;  // padded row stride if it fits
+  constexpr int RFIT = EB / LDE;
+  constexpr int RPP = RFIT >= BM ? BM : RFIT >= 128 && BM % 128 == 0 ? 128
+                    : RFIT >= 64 && BM % 64 == 0 ? 64 : 32;  // rows per pass, dividing BM
+  static_assert(RFIT >= 32 && BM % RPP == 0, "epilogue pass must hold 32-row blocks");
   constexpr int PIECES_PER_ROW = BN / C::EPP;  // 16-byte output pieces per row
-  unsigned char* sE = r0;
+  unsigned char* sE = ring_mem;
 #pragma unroll
   for (int p0 = 0; p0 < BM; p0 += RPP) {
 #pragma unroll
