@@ -571,11 +571,15 @@ struct ColumnLookup {
 // [c_first + (kd-1)*dD*Y - dH, c_last + (kd-1)*dD*Y + dH], and the sorted voxels of those
 // columns are one contiguous run of the sorted arrays.  Phase 1 decodes the block's voxels once
 // (column, z, row, a 9-bit mask of in-grid neighbor columns, the duplicate check) and copies,
-// per kd, that run's z values and rows plus the column starts into LDS with coalesced loads.
+// per kd, that run's rows and keys relative to the window's first column (j*Z + z for the j-th
+// column of the window; keys are unique, so a relative key names one voxel) plus the column
+// starts into LDS with coalesced loads; sentinel keys above every real one pad the run.
 // Phase 2 resolves every probe from LDS with 9 lanes per voxel (one per neighbor column, as in
-// the column-parallel fill): a binary search for the first z >= z - dW in the column, then at
-// most 2*dW + 1 consecutive entries.  A kd window that does not fit (very sparse or very dense
-// regions) falls back to the global column lookup for that kd only.
+// the column-parallel fill): a binary search for the first key >= the lowest wanted one in the
+// column, then at most 2*dW + 1 consecutive entries, compared as keys (an entry of another
+// column or a sentinel cannot equal a wanted key).  A kd window that does not fit (very sparse or
+// very dense regions, or Z so large that window keys overflow 31 bits) falls back to the global
+// column lookup for that kd only.
 constexpr int kWinThreads = 256;
 constexpr int kWinRounds = 4;
 constexpr int kWinVox = kWinRounds * mapk::kFillVoxPerWave * (kWinThreads / 64);  // 112
@@ -589,8 +593,10 @@ __global__ void __launch_bounds__(kWinThreads)
                        int32_t dD, int32_t dH, int32_t dW, int64_t ncol, int32_t per_xcd,
                        int32_t* __restrict__ nbr, uint32_t* __restrict__ status) {
   using I = typename std::conditional<sizeof(K) == 4, int32_t, int64_t>::type;  // column index
-  __shared__ int32_t lz[3][kWinCapE + 4];  // +4: the probe reads up to 2 past a column's end
-  __shared__ int32_t lp[3][kWinCapE + 4];
+  // Window keys / rows at [1, ne], slot 0 readable (never used), sentinels after the run: the
+  // probe reads up to 2 past a column's end and its search one before the column's start.
+  __shared__ int32_t lk[3][kWinCapE + 5];
+  __shared__ int32_t lp[3][kWinCapE + 5];
   __shared__ int32_t lcs[3][kWinCapC + 1];
   __shared__ I w_lo[3];
   __shared__ int32_t w_e0[3], w_ne[3], w_nc[3];
@@ -637,7 +643,9 @@ __global__ void __launch_bounds__(kWinThreads)
     if (lo < 0) lo = 0;
     if (hi > ncol - 1) hi = ncol - 1;
     int32_t e0 = 0, ne = 0, nc = 0;
-    if (lo <= hi && hi - lo + 1 <= kWinCapC) {
+    // Window keys (j*Z + z) must stay below 2^31 - 1 (the sentinel).
+    const bool keys31 = (int64_t)(kWinCapC + 1) * Z < (int64_t)INT32_MAX;
+    if (lo <= hi && hi - lo + 1 <= kWinCapC && keys31) {
       e0 = col_start[lo];
       ne = col_start[hi + 1] - e0;
       nc = (int32_t)(hi - lo + 1);
@@ -657,11 +665,13 @@ __global__ void __launch_bounds__(kWinThreads)
     if (nc <= 0) continue;
     const I lo = w_lo[w];
     const int32_t e0 = w_e0[w], ne = w_ne[w];
+    const K kbase = (K)lo * (K)Z;  // key of the window's first column at z = 0
     for (int j = tid; j <= nc; j += kWinThreads) lcs[w][j] = col_start[lo + j] - e0;
     for (int j = tid; j < ne; j += kWinThreads) {
-      lz[w][j] = kc_.z_of(keys[e0 + j]);
-      lp[w][j] = perm[e0 + j];
+      lk[w][1 + j] = (int32_t)(keys[e0 + j] - kbase);
+      lp[w][1 + j] = perm[e0 + j];
     }
+    if (tid < 4) lk[w][1 + ne + tid] = INT32_MAX;
   }
   __syncthreads();
 
@@ -683,18 +693,20 @@ __global__ void __launch_bounds__(kWinThreads)
   const int nc_w = w_nc[kd];
   const I lo_w = w_lo[kd];
   const I off = (I)(kd - 1) * dD * Y + (I)(kh - 1) * dH;
-  const int32_t* const wz = lz[kd];
-  const int32_t* const wp = lp[kd];
+  const int32_t* const wk = lk[kd] + 1;
+  const int32_t* const wp = lp[kd] + 1;
   const int32_t* const wc = lcs[kd];
   const int li0 = wid * kWinRounds * mapk::kFillVoxPerWave + slot;
   if (dW == 1 && w_nc[0] >= 0 && w_nc[1] >= 0 && w_nc[2] >= 0) {
-    // Every window fits (block-uniform): branch-free probes.  A column's first entry with
-    // z >= z-1 comes from a binary search with a block-uniform step count (powers of two below
-    // the longest column); the taps z-1, z, z+1 can only be that entry and the next two.
+    // Every window fits (block-uniform): branch-free probes.  The neighbor column is window
+    // column j (an in-grid neighbor column always lies in the window) and the wanted keys are
+    // t - 1, t, t + 1 with t = j*Z + z.  The first entry >= t - 1 comes from a binary search
+    // over the column with a block-uniform step count (powers of two below the longest column);
+    // the three keys can only be that entry and the next two.  Out-of-grid lanes search an empty
+    // range and want negative keys, which match nothing.
     int steps = 0;
     while ((2 << steps) <= w_maxlen) ++steps;  // 2^steps <= maxlen < 2^(steps+1)
     const int top = w_maxlen > 0 ? 1 << steps : 0;
-    const int jmax = nc_w > 0 ? nc_w - 1 : 0;
 #pragma unroll
     for (int r = 0; r < kWinRounds; ++r) {
       const int li = li0 + r * mapk::kFillVoxPerWave;
@@ -703,32 +715,27 @@ __global__ void __launch_bounds__(kWinThreads)
       const int32_t row = vrow[lic];
       const int32_t z = vz[lic];
       const bool inb = ((vmask[lic] >> col) & 1) && live;
-      int j = (int)(vcol[lic] + off - lo_w);
-      j = j < 0 ? 0 : (j > jmax ? jmax : j);
-      const int a = nc_w > 0 ? wc[j] : 0;  // an empty window (nc_w == 0) has no in-grid column
-      const int e = (inb && nc_w > 0) ? wc[j + 1] : a;
-      const int32_t first = z > 0 ? z - 1 : z;
+      const int j = inb ? (int)(vcol[lic] + off - lo_w) : 0;
+      const int a = inb ? wc[j] : 0;
+      const int e = inb ? wc[j + 1] : 0;
+      const int32_t t = inb ? j * Z + z : -4;
+      const int32_t first = z > 0 ? t - 1 : t;
       int pos = a;
       for (int st = top; st > 0; st >>= 1) {  // uniform trip count, no lane branches
-        const int t = pos + st;
-        int idx = (t < e ? t : e) - 1;
-        idx = idx < 0 ? 0 : idx;
-        const int32_t zv = wz[idx];
-        pos = ((t <= e) & (zv < first)) ? t : pos;
+        const int tt = pos + st;
+        const int32_t kv = wk[(tt < e ? tt : e) - 1];  // index >= a - 1 >= -1
+        pos = ((tt <= e) & (kv < first)) ? tt : pos;
       }
-      // pos <= e <= kWinCapE, so pos + 2 stays inside the padded arrays.
-      const int32_t z0 = wz[pos], z1 = wz[pos + 1], z2 = wz[pos + 2];
+      // pos <= e <= ne: pos + 2 reads a later column's key or a sentinel at worst.
+      const int32_t k0 = wk[pos], k1 = wk[pos + 1], k2 = wk[pos + 2];
       const int32_t p0 = wp[pos], p1 = wp[pos + 1], p2 = wp[pos + 2];
-      const bool ok0 = pos < e, ok1 = pos + 1 < e, ok2 = pos + 2 < e;
-      const int32_t zm = z > 0 ? z - 1 : -2, zp = z + 1 < Z ? z + 1 : -2;
-      // Entries from pos on are >= z-1 (>= z when z == 0) and strictly increasing, so z-1 can
-      // only sit at pos, z at pos or pos+1, z+1 at pos, pos+1 or pos+2.
-      const int32_t v0 = (ok0 & (z0 == zm)) ? p0 : -1;
-      int32_t v1 = (ok0 & (z0 == z)) ? p0 : -1;
-      v1 = (ok1 & (z1 == z)) ? p1 : v1;
-      int32_t v2 = (ok0 & (z0 == zp)) ? p0 : -1;
-      v2 = (ok1 & (z1 == zp)) ? p1 : v2;
-      v2 = (ok2 & (z2 == zp)) ? p2 : v2;
+      const int32_t tm = z > 0 ? t - 1 : -4, tp = z + 1 < Z ? t + 1 : -4;
+      const int32_t v0 = k0 == tm ? p0 : -1;
+      int32_t v1 = k1 == t ? p1 : -1;
+      v1 = k0 == t ? p0 : v1;
+      int32_t v2 = k2 == tp ? p2 : -1;
+      v2 = k1 == tp ? p1 : v2;
+      v2 = k0 == tp ? p0 : v2;
       if (col == 4) v1 = row;  // tap 13 is the voxel itself
       if (live) {
         int32_t* dst = nbr + (int64_t)row * 27 + col * 3;
@@ -755,18 +762,20 @@ __global__ void __launch_bounds__(kWinThreads)
         int a = wc[j];
         int b = wc[j + 1];
         const int e = b;
-        const int32_t first = has_lo ? z - dW : z;
-        while (a < b) {  // first entry with z >= first
+        const int32_t base = j * Z;  // window key of (column j, z = 0)
+        const int32_t first = base + (has_lo ? z - dW : z);
+        while (a < b) {  // first entry with key >= first
           const int mid = (a + b) >> 1;
-          if (wz[mid] < first) a = mid + 1;
+          if (wk[mid] < first) a = mid + 1;
           else b = mid;
         }
-        const int32_t last = has_hi ? z + dW : z;
+        const int32_t last = base + (has_hi ? z + dW : z);
         for (int t = 0; t < nscan; ++t, ++a) {
           if (a >= e) break;
-          const int32_t zz = wz[a];
-          if (zz > last) break;
+          const int32_t kk = wk[a];
+          if (kk > last) break;
           const int32_t p = wp[a];
+          const int32_t zz = kk - base;
           if (zz == z) v1 = p;
           else if (has_lo && zz == z - dW) v0 = p;
           else if (has_hi && zz == z + dW) v2 = p;
