@@ -15,6 +15,7 @@
  *   layerNorm                                         src/dense/ops/layer_norm.ts:12-125
  *   silu                                              src/dense/ops/silu.ts:11-56
  *   add (residual)                                    src/dense/ops/elementwise.ts:22-65
+ *   decoder upsample (1 -> 8 children)                src/models/sparse_unet_vae_decoder.ts:155-175
  */
 #ifndef TSC_H
 #define TSC_H
@@ -26,7 +27,7 @@
 extern "C" {
 #endif
 
-#define TSC_VERSION 1
+#define TSC_VERSION 2
 
 /* Status codes returned by every entry point. */
 enum tsc_status {
@@ -147,6 +148,23 @@ int tsc_resblock(tsc_ctx* ctx, int32_t dtype, const void* x, const int32_t* nbr,
                  const int32_t* order, int64_t N, int32_t C, const void* w1, const void* b1,
                  const void* ln_gamma, const void* ln_beta, float eps, const void* w2,
                  const void* b2, void* out);
+
+/* ---- subdivision (the decoder's upsample step) --------------------------------------------- */
+/* Children of every voxel at twice the resolution: parent row n = [b,x,y,z] gives the rows
+ * [b, 2x+dx, 2y+dy, 2z+dz], c = dx*4 + dy*2 + dz, each with a copy of the parent's feature row.
+ * Rows are parent-major, children in increasing c.  With keep (device uint8 (N); bit c of keep[n]
+ * = keep child c of parent n) only the kept children are written, in the same order.
+ *   coords      device int32 (N,4), 16-byte aligned, x,y,z < 2^30
+ *   feats       device (N,C) `dtype` rows, or NULL for coordinates only
+ *   coords_out  device int32 (M,4), feats_out (M,C): M = 8N without keep, else the number of set
+ *               bits of keep (tsc_subdivide_count; it synchronizes the stream to return it).
+ *               Non-null whenever N > 0 (a host with M == 0 has nothing to call for).
+ * Replaces the upsample step of the sparse decoder (src/models/sparse_unet_vae_decoder.ts:155-175,
+ * where the TS port only doubles the spatial shape); the spatial shape and the scale of the
+ * result are twice the input's. */
+int tsc_subdivide_count(tsc_ctx* ctx, const uint8_t* keep, int64_t N, int64_t* count);
+int tsc_subdivide(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t dtype, const void* feats,
+                  int32_t C, const uint8_t* keep, int32_t* coords_out, void* feats_out);
 
 /* ---- per-kernel timing -------------------------------------------------------------------- */
 /* While enabled, every kernel the context launches is bracketed by hipEvents on its stream.

@@ -11,10 +11,20 @@ Contents
                     index_select + mm), used as the timed CPU baseline
   brute.py          pure-Python brute force for tiny inputs
 
+  subdivide()        numpy restatement of the decoder's upsample step (each voxel -> its 2x2x2
+                    children, optional keep mask)
+
 Pinning (see tests/test_oracle.py): the map builds are checked against each other and against
 brute force, sorted keys against numpy.unique, the conv against a dense torch F.conv3d closed
 form in fp64, LayerNorm/SiLU against torch.nn.functional in fp64, and all of them against the
-fixtures in tests/golden/ that were generated without this package.
+fixtures in tests/golden/ that were generated without this package.  subdivide() is pinned by
+what its definition fixes: every output row's parent is (b, x//2, y//2, z//2) with child index
+from the low bits, the children of a full subdivision are exactly the 8N cells of the doubled
+grid that lie inside parent cells, a dense 2^3 block maps onto a dense 4^3 block, and one
+subdivision equals the union of eight single-child keep masks.  The reference holds no tests or
+fixtures for it (its TS port does not generate children: sparse_unet_vae_decoder.ts:155-175);
+the child order follows torch.nonzero over a 2x2x2 cube (dx slowest, dz fastest), the order of
+trellis2's SparseSubdivide, which is not in this container: that convention is parity unpinned.
 """
 from __future__ import annotations
 
@@ -153,3 +163,23 @@ def resblock(x, nbr, w1, b1, w2, b2, gamma=None, beta=None, eps=1e-6) -> np.ndar
     h = conv(x, w1, b1, nbr)
     h = layernorm(h, gamma, beta, eps, silu=True)
     return np.asarray(x, np.float64) + conv(h, w2, b2, nbr)
+
+
+def subdivide(coords, feats=None, keep=None):
+    """Children at twice the resolution (the decoder's upsample step, caller
+    src/models/sparse_unet_vae_decoder.ts:155-175): parent [b,x,y,z] -> [b, 2x+dx, 2y+dy, 2z+dz]
+    with c = dx*4 + dy*2 + dz, rows parent-major and c increasing, features copied from the
+    parent; keep (uint8 per parent, bit c) selects children.  Returns (coords, feats or None)."""
+    coords = np.asarray(coords, np.int64).reshape(-1, 4)
+    n = coords.shape[0]
+    c = np.arange(8)
+    off = np.stack([np.zeros(8, np.int64), c >> 2, (c >> 1) & 1, c & 1], axis=1)
+    base = coords * np.array([1, 2, 2, 2], np.int64)
+    kids = (base[:, None, :] + off[None, :, :]).reshape(-1, 4)
+    sel = np.ones(8 * n, bool) if keep is None else \
+        ((np.asarray(keep, np.uint8)[:, None] >> c[None, :]) & 1).astype(bool).reshape(-1)
+    out_f = None
+    if feats is not None:
+        f = np.asarray(feats)
+        out_f = np.repeat(f, 8, axis=0)[sel]
+    return kids[sel].astype(np.int32), out_f

@@ -208,3 +208,65 @@ def test_planted_mistakes_are_caught():
     w_t = a[("in", "weight")].transpose(0, 3, 2, 1, 4)
     out_t = oracle.conv(a[("in", "feats")], w_t, a[("in", "bias")], nbr)
     assert not np.allclose(out_t, a[("exp", "conv_out")], rtol=1e-6, atol=1e-6)  # kernel transposed
+
+
+# ---- subdivision (decoder upsample) ---------------------------------------------------------
+
+def _unique_coords(rng, n, batch, shape):
+    cells = rng.choice(batch * shape[0] * shape[1] * shape[2], size=n, replace=False)
+    b, r = np.divmod(cells, shape[0] * shape[1] * shape[2])
+    x, r = np.divmod(r, shape[1] * shape[2])
+    y, z = np.divmod(r, shape[2])
+    return np.stack([b, x, y, z], axis=1).astype(np.int32)
+
+
+def test_subdivide_parent_and_child_index_of_every_row():
+    rng = np.random.default_rng(3)
+    c = _unique_coords(rng, 300, 3, (9, 7, 11))
+    f = rng.standard_normal((300, 5)).astype(np.float32)
+    kids, kf = oracle.subdivide(c, f)
+    assert kids.shape == (2400, 4)
+    rows = np.arange(2400)
+    par = c[rows // 8]
+    np.testing.assert_array_equal(kids[:, 0], par[:, 0])
+    np.testing.assert_array_equal(kids[:, 1:] // 2, par[:, 1:])
+    child = (kids[:, 1] & 1) * 4 + (kids[:, 2] & 1) * 2 + (kids[:, 3] & 1)
+    np.testing.assert_array_equal(child, rows % 8)
+    np.testing.assert_array_equal(kf, f[rows // 8])
+
+
+def test_subdivide_children_are_the_doubled_cells_inside_parents():
+    """Brute force over every cell of the doubled grid."""
+    rng = np.random.default_rng(4)
+    shape = (3, 4, 2)
+    c = _unique_coords(rng, 7, 2, shape)
+    parents = {tuple(r) for r in c.tolist()}
+    want = {(b, x, y, z) for b in range(2) for x in range(6) for y in range(8) for z in range(4)
+            if (b, x // 2, y // 2, z // 2) in parents}
+    kids, _ = oracle.subdivide(c)
+    got = [tuple(r) for r in kids.tolist()]
+    assert len(got) == len(set(got)) == 8 * len(c)
+    assert set(got) == want
+
+
+def test_subdivide_dense_block_and_keep_masks():
+    block = np.array([[0, x, y, z] for x in range(2) for y in range(2) for z in range(2)], np.int32)
+    kids, _ = oracle.subdivide(block)
+    assert {tuple(r) for r in kids.tolist()} == {(0, x, y, z) for x in range(4) for y in range(4)
+                                                 for z in range(4)}
+    rng = np.random.default_rng(5)
+    c = _unique_coords(rng, 50, 1, (6, 6, 6))
+    f = rng.standard_normal((50, 3)).astype(np.float32)
+    full, ff = oracle.subdivide(c, f)
+    # eight single-child masks interleave back into the full subdivision
+    singles = [oracle.subdivide(c, f, np.full(50, 1 << ch, np.uint8)) for ch in range(8)]
+    inter = np.stack([s[0] for s in singles], axis=1).reshape(-1, 4)
+    np.testing.assert_array_equal(inter, full)
+    np.testing.assert_array_equal(np.stack([s[1] for s in singles], axis=1).reshape(-1, 3), ff)
+    # a random mask keeps exactly its set bits, in parent-major order
+    keep = rng.integers(0, 256, size=50).astype(np.uint8)
+    kk, kf = oracle.subdivide(c, f, keep)
+    bits = np.unpackbits(keep[:, None], axis=1, bitorder="little").astype(bool).reshape(-1)
+    np.testing.assert_array_equal(kk, full[bits])
+    np.testing.assert_array_equal(kf, ff[bits])
+    assert oracle.subdivide(c, None, np.zeros(50, np.uint8))[0].shape == (0, 4)

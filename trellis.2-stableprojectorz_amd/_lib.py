@@ -63,6 +63,8 @@ _SIGNATURES = {
     "tsc_silu": (_I32, [_P, _I32, _P, _I64, _P]),
     "tsc_add": (_I32, [_P, _I32, _P, _P, _I64, _P]),
     "tsc_resblock": (_I32, [_P, _I32, _P, _P, _P, _I64, _I32, _P, _P, _P, _P, _F32, _P, _P, _P]),
+    "tsc_subdivide_count": (_I32, [_P, _P, _I64, ctypes.POINTER(_I64)]),
+    "tsc_subdivide": (_I32, [_P, _P, _I64, _I32, _P, _I32, _P, _P, _P]),
     "tsc_profile_enable": (_I32, [_P, _I32]),
     "tsc_profile_collect": (_I32, [_P, ctypes.POINTER(_I32)]),
     "tsc_profile_entry": (_I32, [_P, _I32, ctypes.c_char_p, _I32, ctypes.POINTER(ctypes.c_double),

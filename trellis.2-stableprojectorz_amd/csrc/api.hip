@@ -399,6 +399,42 @@ int tsc_resblock(tsc_ctx* ctx, int32_t dtype, const void* x, const int32_t* nbr,
   return conv_launch(ctx, a2);
 }
 
+int tsc_subdivide_count(tsc_ctx* ctx, const uint8_t* keep, int64_t N, int64_t* count) {
+  g_err[0] = 0;
+  int st = check_ctx(ctx);
+  if (st) return st;
+  if (N < 0 || !count) return fail(TSC_ERR_INVALID, "subdivide_count: bad arguments");
+  if (N > 0 && !keep) return fail(TSC_ERR_INVALID, "subdivide_count: null keep mask");
+  DeviceGuard g(ctx->device);
+  return subdivide_count_launch(ctx, keep, N, count);
+}
+
+int tsc_subdivide(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t dtype, const void* feats,
+                  int32_t C, const uint8_t* keep, int32_t* coords_out, void* feats_out) {
+  g_err[0] = 0;
+  int st = check_ctx(ctx);
+  if (st) return st;
+  if (N < 0) return fail(TSC_ERR_INVALID, "subdivide: negative N");
+  if (N == 0) return TSC_OK;
+  if (!coords || !coords_out) return fail(TSC_ERR_INVALID, "subdivide: null coordinate buffer");
+  if (!aligned(coords, 16) || !aligned(coords_out, 16))
+    return fail(TSC_ERR_INVALID, "subdivide: coordinate buffers must be 16-byte aligned");
+  int64_t row_bytes = 0;
+  if (feats) {
+    if (!elem_size(dtype)) return fail(TSC_ERR_INVALID, "subdivide: unknown dtype %d", dtype);
+    if (C <= 0) return fail(TSC_ERR_INVALID, "subdivide: C must be positive, got %d", C);
+    if (!feats_out) return fail(TSC_ERR_INVALID, "subdivide: null feats_out");
+    row_bytes = (int64_t)C * elem_size(dtype);
+    if (row_bytes > (int64_t)1 << 20)
+      return fail(TSC_ERR_UNSUPPORTED, "subdivide: feature rows above 1 MiB (C=%d)", C);
+    const size_t piece = row_bytes % 16 == 0 ? 16 : row_bytes % 4 == 0 ? 4 : 2;
+    if (!aligned(feats, piece) || !aligned(feats_out, piece))
+      return fail(TSC_ERR_INVALID, "subdivide: feature buffers must be %zu-byte aligned", piece);
+  }
+  DeviceGuard g(ctx->device);
+  return subdivide_launch(ctx, coords, N, feats, row_bytes, keep, coords_out, feats_out);
+}
+
 int tsc_profile_enable(tsc_ctx* ctx, int on) {
   g_err[0] = 0;
   int st = check_ctx(ctx);

@@ -107,6 +107,12 @@ struct ConvArgs {
 };
 int conv_launch(tsc_ctx* ctx, const ConvArgs& a);
 
+// ---- launchers implemented in subdivide.hip ----
+int subdivide_count_launch(tsc_ctx* ctx, const uint8_t* keep, int64_t N, int64_t* count_host);
+int subdivide_launch(tsc_ctx* ctx, const int32_t* coords, int64_t N, const void* feats,
+                     int64_t row_bytes, const uint8_t* keep, int32_t* coords_out,
+                     void* feats_out);
+
 // ---- launchers implemented in rowops.hip ----
 int layernorm_launch(tsc_ctx* ctx, int32_t dtype, const void* x, int64_t N, int32_t C,
                      const void* gamma, const void* beta, float eps, int32_t apply_silu, void* y);

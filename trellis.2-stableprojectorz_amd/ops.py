@@ -207,3 +207,43 @@ def sparse_resblock(x: torch.Tensor, nmap, w1, b1, w2, b2, ln_weight=None, ln_bi
     check(ctx.lib.tsc_resblock(ctx.bind(), _code(x), _p(x), _p(nbr), _p(order), n, c, _p(w1), _p(b1),
                                _p(ln_weight), _p(ln_bias), float(eps), _p(w2), _p(b2), _p(out)))
     return out
+
+
+def subdivide_count(keep: torch.Tensor) -> int:
+    """Number of children a keep mask selects (uint8 (N,), bit c = child c); one stream sync."""
+    if keep.dtype != torch.uint8 or keep.dim() != 1:
+        raise TscError(_lib.TSC_ERR_INVALID, "keep must be uint8 of shape (N,)")
+    ctx = _lib.context(_dev(keep))
+    out = ctypes.c_int64(0)
+    check(ctx.lib.tsc_subdivide_count(ctx.bind(), _p(keep), keep.shape[0], ctypes.byref(out)))
+    return int(out.value)
+
+
+def sparse_subdivide(coords: torch.Tensor, feats: torch.Tensor | None = None,
+                     keep: torch.Tensor | None = None):
+    """Children at twice the resolution (tsc_subdivide): (coords_out (M,4), feats_out (M,C)).
+
+    Parent [b,x,y,z] -> children [b, 2x+dx, 2y+dy, 2z+dz], c = dx*4 + dy*2 + dz, parent-major,
+    each with a copy of the parent's feature row; keep (uint8 (N,), bit c = keep child c) selects
+    children (M = its set bits; counting them costs one stream sync), else M = 8N.
+    """
+    if coords.dtype != torch.int32 or coords.dim() != 2 or coords.shape[1] != 4:
+        raise TscError(_lib.TSC_ERR_INVALID, "coords must be int32 of shape (N,4)")
+    if feats is not None and (feats.dim() != 2 or feats.shape[0] != coords.shape[0]):
+        raise TscError(_lib.TSC_ERR_INVALID, "feats must be (N,C) with the coords' N")
+    if keep is not None and (keep.dtype != torch.uint8 or keep.shape != (coords.shape[0],)):
+        raise TscError(_lib.TSC_ERR_INVALID, "keep must be uint8 of shape (N,)")
+    dev = _dev(coords, feats, keep)
+    ctx = _lib.context(dev)
+    n = coords.shape[0]
+    m = 8 * n if keep is None else subdivide_count(keep)
+    coords_out = torch.empty((m, 4), dtype=torch.int32, device=coords.device)
+    feats_out = None
+    dtype, c = 0, 0
+    if feats is not None:
+        dtype, c = _code(feats), feats.shape[1]
+        feats_out = torch.empty((m, c), dtype=feats.dtype, device=feats.device)
+    if m:
+        check(ctx.lib.tsc_subdivide(ctx.bind(), _p(coords), n, dtype, _p(feats), c, _p(keep),
+                                    _p(coords_out), _p(feats_out)))
+    return coords_out, feats_out
