@@ -12,6 +12,8 @@ TFLOP/s counting only valid taps, algorithmic GB/s, roofline fraction):
   narrow512_f16    conv 32->32 and 32->64 fp16 on the map512 voxels
   wide128_bf16     conv 512->512 bf16, 4 x ~61k voxels (128^3 shells)
   resblock64_bf16  4 x ResBlock (conv-LN-SiLU-conv-+x) at C=1024 bf16, 2 x ~32k voxels
+and the decoder upsample (tsc_subdivide) on the wide128 voxels with 512 bf16 channels, all 8
+children and a random keep mask (ms, algorithmic GB/s = coords + rows in and out, HBM fraction).
 
 `roofline` is for the map build's dominant kernel, timed with hipEvents around each launch on
 the stream the library launches on; `cpu_baseline` times the PyTorch-CPU restatement of the
@@ -135,6 +137,55 @@ def profile_pass(pkg, dev) -> None:
             pkg.sparse_conv3d(f, wt, None, nmap)
         torch.cuda.synchronize()
         log(f"{name} conv done")
+    sc = torch.from_numpy(wl.make_coords("wide128_bf16")).to(dev)
+    sf = torch.randn((sc.shape[0], SUBDIV_C), device=dev).to(torch.bfloat16)
+    for _ in range(2):
+        pkg.sparse_subdivide(sc, sf)
+    torch.cuda.synchronize()
+    log("subdivide done")
+
+
+# Decoder upsample measured on the 2-voxel shell in 128^3 (4 x ~60k voxels) with 512 bf16
+# channels: every voxel -> its 8 children, then a random keep mask (~half the children).
+SUBDIV_C = 512
+
+
+def subdivide_records(pkg, dev, steps, warmup) -> list:
+    import numpy as np
+    import torch
+
+    wl = pkg.workloads
+    coords = wl.make_coords("wide128_bf16")
+    n = coords.shape[0]
+    c = torch.from_numpy(coords).to(dev)
+    f = torch.from_numpy(wl.features(n, SUBDIV_C, 4)).to(dev).to(torch.bfloat16)
+    keep = torch.from_numpy(np.random.default_rng(5).integers(0, 256, n).astype(np.uint8)).to(dev)
+    row = SUBDIV_C * 2
+    out = []
+    ctx = pkg._lib.context(dev.index)
+    for label, k in (("all 8 children", None), ("random keep mask", keep)):
+        m = 8 * n if k is None else pkg.subdivide_count(k)
+        co = torch.empty((m, 4), dtype=torch.int32, device=dev)
+        fo = torch.empty((m, SUBDIV_C), dtype=torch.bfloat16, device=dev)
+
+        def run():
+            pkg._lib.check(ctx.lib.tsc_subdivide(ctx.bind(), c.data_ptr(), n, 2, f.data_ptr(),
+                                                 SUBDIV_C, None if k is None else k.data_ptr(),
+                                                 co.data_ptr(), fo.data_ptr()))
+        ms = time_steps(run, steps, warmup)
+        nbytes = n * (16 + row) + m * (16 + row) + (0 if k is None else n)
+        rec = {"workload": f"subdivide wide128 shell, {SUBDIV_C} bf16 channels, {label}",
+               "voxels": n, "children": m, "ms": round(ms, 4),
+               "gbps_algorithmic": round(nbytes / (ms / 1e3) / 1e9, 1), "bound": "hbm",
+               "roofline_frac": round(nbytes / (ms / 1e3) / PEAK_HBM, 4),
+               "kernels": {kn: {"avg_ms": round(a, 4), "launches_per_step": cnt}
+                           for kn, (a, cnt) in kernel_times(ctx, run, 3).items()}}
+        log(f"subdivide ({label}): {ms:.4f} ms, {rec['gbps_algorithmic']} GB/s, "
+            f"roofline {rec['roofline_frac']}")
+        out.append(rec)
+        del co, fo
+        torch.cuda.empty_cache()
+    return out
 
 
 def cpu_baseline(coords_np, shape, threads: int) -> dict:
@@ -294,6 +345,7 @@ def main() -> int:
     sec = []
     if not args.no_secondary:
         sec = secondary(pkg, dev, args.steps, args.warmup, coords)
+        sec += subdivide_records(pkg, dev, args.steps, args.warmup)
     cpu = None
     if not args.no_cpu_baseline:
         log(f"cpu baseline on {args.cpu_threads} threads ...")
