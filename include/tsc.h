@@ -16,6 +16,8 @@
  *   silu                                              src/dense/ops/silu.ts:11-56
  *   add (residual)                                    src/dense/ops/elementwise.ts:22-65
  *   decoder upsample (1 -> 8 children)                src/models/sparse_unet_vae_decoder.ts:155-175
+ *   sparseLinear / ConvNeXt block linears             src/sparse/ops/linear.ts:9-29,
+ *                                                     src/models/sparse_unet_vae_decoder.ts:48-78
  */
 #ifndef TSC_H
 #define TSC_H
@@ -148,6 +150,15 @@ int tsc_resblock(tsc_ctx* ctx, int32_t dtype, const void* x, const int32_t* nbr,
                  const int32_t* order, int64_t N, int32_t C, const void* w1, const void* b1,
                  const void* ln_gamma, const void* ln_beta, float eps, const void* w2,
                  const void* b2, void* out);
+
+/* ---- per-voxel linear layer ---------------------------------------------------------------- */
+/* out (N,Cout) = x (N,Cin) * weight^T + bias (+ residual); weight (Cout,Cin) as nn.Linear, bias
+ * (Cout) or NULL, residual (N,Cout) or NULL (it may alias out; x may not).  All `dtype`, fp32
+ * accumulation, one hipBLASLt GEMM (bias epilogue, residual as its C operand).
+ * Replaces sparseLinear (src/sparse/ops/linear.ts:9-29) and the matmul + add pairs of the sparse
+ * ConvNeXt block (src/models/sparse_unet_vae_decoder.ts:48-78). */
+int tsc_linear(tsc_ctx* ctx, int32_t dtype, const void* x, int64_t N, int32_t Cin,
+               const void* weight, const void* bias, const void* residual, int32_t Cout, void* out);
 
 /* ---- subdivision (the decoder's upsample step) --------------------------------------------- */
 /* Children of every voxel at twice the resolution: parent row n = [b,x,y,z] gives the rows

@@ -13,6 +13,8 @@ Contents
 
   subdivide()        numpy restatement of the decoder's upsample step (each voxel -> its 2x2x2
                     children, optional keep mask)
+  linear(), convnext_block()
+                    fp64 numpy restatements of nn.Linear per voxel and the sparse ConvNeXt block
 
 Pinning (see tests/test_oracle.py): the map builds are checked against each other and against
 brute force, sorted keys against numpy.unique, the conv against a dense torch F.conv3d closed
@@ -25,6 +27,9 @@ subdivision equals the union of eight single-child keep masks.  The reference ho
 fixtures for it (its TS port does not generate children: sparse_unet_vae_decoder.ts:155-175);
 the child order follows torch.nonzero over a 2x2x2 cube (dx slowest, dz fastest), the order of
 trellis2's SparseSubdivide, which is not in this container: that convention is parity unpinned.
+linear() is pinned against torch.nn.functional.linear in fp64; convnext_block() is the
+composition of the pinned conv, layernorm and linear (the block's step order is the TS port's,
+sparse_unet_vae_decoder.ts:48-78).
 """
 from __future__ import annotations
 
@@ -183,3 +188,28 @@ def subdivide(coords, feats=None, keep=None):
         f = np.asarray(feats)
         out_f = np.repeat(f, 8, axis=0)[sel]
     return kids[sel].astype(np.int32), out_f
+
+
+def linear(x, weight, bias=None, residual=None) -> np.ndarray:
+    """x (N,Cin) @ weight(Cout,Cin)^T + bias (+ residual), fp64 (nn.Linear per voxel,
+    src/sparse/ops/linear.ts:9-29)."""
+    y = np.asarray(x, np.float64) @ np.asarray(weight, np.float64).T
+    if bias is not None:
+        y = y + np.asarray(bias, np.float64)
+    if residual is not None:
+        y = y + np.asarray(residual, np.float64)
+    return y
+
+
+def convnext_block(feats, nbr, conv_w, conv_b, w0, b0, w2, b2, eps=1e-6, rows=None):
+    """Sparse ConvNeXt block (src/models/sparse_unet_vae_decoder.ts:48-78), fp64:
+    h = conv(x); h = LN(h); h = h W0^T + b0; h = silu(LN(h)); out = x + h W2^T + b2.
+    rows: optional subset of output rows (the conv reads neighbors from all of feats)."""
+    f = np.asarray(feats, np.float64)
+    nb = np.asarray(nbr) if rows is None else np.asarray(nbr)[rows]
+    h = conv(f, conv_w, conv_b, nb)
+    h = layernorm(h, None, None, eps)
+    h = linear(h, w0, b0)
+    h = layernorm(h, None, None, eps, silu=True)
+    skip = f if rows is None else f[rows]
+    return linear(h, w2, b2, skip)

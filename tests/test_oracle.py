@@ -270,3 +270,17 @@ def test_subdivide_dense_block_and_keep_masks():
     np.testing.assert_array_equal(kk, full[bits])
     np.testing.assert_array_equal(kf, ff[bits])
     assert oracle.subdivide(c, None, np.zeros(50, np.uint8))[0].shape == (0, 4)
+
+
+def test_linear_vs_torch_functional():
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((40, 24))
+    w = rng.standard_normal((12, 24))
+    b = rng.standard_normal(12)
+    r = rng.standard_normal((40, 12))
+    want = F.linear(torch.from_numpy(x), torch.from_numpy(w), torch.from_numpy(b)).numpy()
+    np.testing.assert_allclose(oracle.linear(x, w, b), want, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(oracle.linear(x, w, b, r), want + r, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(oracle.linear(x, w), x @ w.T, rtol=1e-12, atol=1e-12)
+    # a transposed weight is caught
+    assert not np.allclose(oracle.linear(x[:, :12], w[:, :12].T.copy()), x[:, :12] @ w[:, :12].T)

@@ -7,19 +7,24 @@ is not a Python identifier.
   build_neighbor_map, sparse_conv3d,             functional entry points, one C-ABI call each
   layer_norm, silu, add, sparse_resblock
   SparseSubdivide, sparse_subdivide              decoder upsample (sparse_unet_vae_decoder.ts:155-175)
+  SparseLinear, SparseConvNeXtBlock3d,           decoder blocks (linear.ts:9-29,
+  sparse_linear                                  sparse_unet_vae_decoder.ts:48-78)
   workloads                                      seeded synthetic voxel shells
 """
 from ._lib import TscError, load_library, header_symbols, LIB_PATH  # noqa: F401
 from .sparse_tensor import SparseTensor, Scale, Fraction, SCALE_IDENTITY, compute_layout  # noqa: F401
 from .conv3d import SparseConv3d, SparseResBlock3d, get_neighbor_map, neighbor_cache_key  # noqa: F401
 from .ops import (NeighborMap, build_neighbor_map, map_conv_order, sparse_conv3d,  # noqa: F401
-                  layer_norm, silu, add, sparse_resblock, sparse_subdivide, subdivide_count)
+                  layer_norm, silu, add, sparse_resblock, sparse_subdivide, subdivide_count,
+                  sparse_linear)
 from .spatial import SparseSubdivide  # noqa: F401
+from .blocks import SparseLinear, SparseConvNeXtBlock3d  # noqa: F401
 from . import workloads  # noqa: F401
 
 __all__ = [
     "TscError", "SparseTensor", "SparseConv3d", "SparseResBlock3d", "NeighborMap",
     "build_neighbor_map", "map_conv_order", "sparse_conv3d", "layer_norm", "silu", "add", "sparse_resblock",
-    "sparse_subdivide", "subdivide_count", "SparseSubdivide",
+    "sparse_subdivide", "subdivide_count", "SparseSubdivide", "sparse_linear", "SparseLinear",
+    "SparseConvNeXtBlock3d",
     "get_neighbor_map", "neighbor_cache_key", "workloads",
 ]

@@ -63,6 +63,7 @@ _SIGNATURES = {
     "tsc_silu": (_I32, [_P, _I32, _P, _I64, _P]),
     "tsc_add": (_I32, [_P, _I32, _P, _P, _I64, _P]),
     "tsc_resblock": (_I32, [_P, _I32, _P, _P, _P, _I64, _I32, _P, _P, _P, _P, _F32, _P, _P, _P]),
+    "tsc_linear": (_I32, [_P, _I32, _P, _I64, _I32, _P, _P, _P, _I32, _P]),
     "tsc_subdivide_count": (_I32, [_P, _P, _I64, ctypes.POINTER(_I64)]),
     "tsc_subdivide": (_I32, [_P, _P, _I64, _I32, _P, _I32, _P, _P, _P]),
     "tsc_profile_enable": (_I32, [_P, _I32]),

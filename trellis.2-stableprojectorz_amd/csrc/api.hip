@@ -66,6 +66,10 @@ int sched_workspace(tsc_ctx* ctx, size_t bytes, void** out) {
   return grow_buffer(ctx, &ctx->ws_sched, &ctx->ws_sched_bytes, bytes, "schedule workspace", out);
 }
 
+int blas_workspace(tsc_ctx* ctx, size_t bytes, void** out) {
+  return grow_buffer(ctx, &ctx->ws_blas, &ctx->ws_blas_bytes, bytes, "hipBLASLt workspace", out);
+}
+
 void prof_clear(tsc_ctx* ctx) {
   for (auto& r : ctx->prof) {
     (void)hipEventDestroy(r.start);
@@ -162,6 +166,8 @@ int tsc_ctx_destroy(tsc_ctx* ctx) {
   int st = check_hip(hipStreamSynchronize(ctx->stream), "ctx_destroy sync");
   if (ctx->ws) (void)hipFree(ctx->ws);
   if (ctx->ws_sched) (void)hipFree(ctx->ws_sched);
+  blas_destroy(ctx);
+  if (ctx->ws_blas) (void)hipFree(ctx->ws_blas);
   prof_clear(ctx);
   delete ctx;
   return st;
@@ -397,6 +403,20 @@ int tsc_resblock(tsc_ctx* ctx, int32_t dtype, const void* x, const int32_t* nbr,
   if (st) return st;
   ConvArgs a2{dtype, h, w2, b2, nbr, order, N, C, C, TSC_EPI_BIAS_RESIDUAL, x, out};
   return conv_launch(ctx, a2);
+}
+
+int tsc_linear(tsc_ctx* ctx, int32_t dtype, const void* x, int64_t N, int32_t Cin,
+               const void* weight, const void* bias, const void* residual, int32_t Cout, void* out) {
+  g_err[0] = 0;
+  int st = check_ctx(ctx);
+  if (st) return st;
+  if (!elem_size(dtype)) return fail(TSC_ERR_INVALID, "linear: unknown dtype %d", dtype);
+  if (N < 0 || Cin <= 0 || Cout <= 0)
+    return fail(TSC_ERR_INVALID, "linear: bad shape N=%lld Cin=%d Cout=%d", (long long)N, Cin, Cout);
+  if (N > 0 && (!x || !weight || !out)) return fail(TSC_ERR_INVALID, "linear: null buffer");
+  if (x == out) return fail(TSC_ERR_INVALID, "linear: out must not alias x");
+  DeviceGuard g(ctx->device);
+  return linear_launch(ctx, dtype, x, N, Cin, weight, bias, residual, Cout, out);
 }
 
 int tsc_subdivide_count(tsc_ctx* ctx, const uint8_t* keep, int64_t N, int64_t* count) {

@@ -31,6 +31,10 @@ struct tsc_ctx {
   // intermediate rows of a ResBlock).
   void* ws_sched = nullptr;
   size_t ws_sched_bytes = 0;
+  // hipBLASLt handle (created on the first linear layer) and its workspace.
+  void* blaslt = nullptr;
+  void* ws_blas = nullptr;
+  size_t ws_blas_bytes = 0;
   bool profile = false;
   std::vector<tsc_prof_rec> prof;      // pending launches
   std::vector<tsc_prof_agg> prof_agg;  // aggregated by tsc_profile_collect
@@ -44,8 +48,9 @@ int check_hip(hipError_t e, const char* what);
 
 // Ensures ctx->ws holds at least `bytes`; returns TSC_OK or an error status.
 int workspace(tsc_ctx* ctx, size_t bytes, void** out);
-// The same for ctx->ws_sched.
+// The same for ctx->ws_sched and ctx->ws_blas.
 int sched_workspace(tsc_ctx* ctx, size_t bytes, void** out);
+int blas_workspace(tsc_ctx* ctx, size_t bytes, void** out);
 
 void prof_clear(tsc_ctx* ctx);
 
@@ -112,6 +117,12 @@ int subdivide_count_launch(tsc_ctx* ctx, const uint8_t* keep, int64_t N, int64_t
 int subdivide_launch(tsc_ctx* ctx, const int32_t* coords, int64_t N, const void* feats,
                      int64_t row_bytes, const uint8_t* keep, int32_t* coords_out,
                      void* feats_out);
+
+// ---- implemented in linear.hip ----
+int linear_launch(tsc_ctx* ctx, int32_t dtype, const void* x, int64_t N, int32_t Cin,
+                  const void* weight, const void* bias, const void* residual, int32_t Cout,
+                  void* out);
+void blas_destroy(tsc_ctx* ctx);
 
 // ---- launchers implemented in rowops.hip ----
 int layernorm_launch(tsc_ctx* ctx, int32_t dtype, const void* x, int64_t N, int32_t C,

@@ -247,3 +247,26 @@ def sparse_subdivide(coords: torch.Tensor, feats: torch.Tensor | None = None,
         check(ctx.lib.tsc_subdivide(ctx.bind(), _p(coords), n, dtype, _p(feats), c, _p(keep),
                                     _p(coords_out), _p(feats_out)))
     return coords_out, feats_out
+
+
+def sparse_linear(x: torch.Tensor, weight: torch.Tensor, bias=None, residual=None,
+                  out=None) -> torch.Tensor:
+    """out (N,Cout) = x (N,Cin) @ weight.T + bias (+ residual) (tsc_linear, one hipBLASLt GEMM);
+    weight (Cout,Cin) as nn.Linear.  out may alias residual."""
+    if x.dim() != 2 or weight.dim() != 2 or weight.shape[1] != x.shape[1]:
+        raise TscError(_lib.TSC_ERR_INVALID, f"linear: x {tuple(x.shape)} vs weight {tuple(weight.shape)}")
+    n, cin = x.shape
+    cout = weight.shape[0]
+    if bias is not None and bias.shape != (cout,):
+        raise TscError(_lib.TSC_ERR_INVALID, "linear: bias must be (Cout,)")
+    if residual is not None and residual.shape != (n, cout):
+        raise TscError(_lib.TSC_ERR_INVALID, "linear: residual must be (N,Cout)")
+    for t in (weight, bias, residual):
+        if t is not None and t.dtype != x.dtype:
+            raise TscError(_lib.TSC_ERR_INVALID, "linear: dtype mismatch")
+    if out is None:
+        out = torch.empty((n, cout), dtype=x.dtype, device=x.device)
+    ctx = _lib.context(_dev(x, weight, bias, residual, out))
+    check(ctx.lib.tsc_linear(ctx.bind(), _code(x), _p(x), n, cin, _p(weight), _p(bias),
+                             _p(residual), cout, _p(out)))
+    return out
