@@ -13,7 +13,8 @@ TFLOP/s counting only valid taps, algorithmic GB/s, roofline fraction):
   wide128_bf16     conv 512->512 bf16, 4 x ~61k voxels (128^3 shells)
   resblock64_bf16  4 x ResBlock (conv-LN-SiLU-conv-+x) at C=1024 bf16, 2 x ~32k voxels
 and the decoder upsample (tsc_subdivide) on the wide128 voxels with 512 bf16 channels, all 8
-children and a random keep mask (ms, algorithmic GB/s = coords + rows in and out, HBM fraction).
+children and a random keep mask (ms, algorithmic GB/s = coords + rows in and out, HBM fraction),
+and a sparse ConvNeXt block (conv + two linears, C=512, hidden 2048, bf16) on the same voxels.
 
 `roofline` is for the map build's dominant kernel, timed with hipEvents around each launch on
 the stream the library launches on; `cpu_baseline` times the PyTorch-CPU restatement of the
@@ -188,6 +189,47 @@ def subdivide_records(pkg, dev, steps, warmup) -> list:
     return out
 
 
+CONVNEXT_C, CONVNEXT_HIDDEN = 512, 2048
+
+
+def convnext_record(pkg, dev, steps, warmup) -> dict:
+    """Sparse ConvNeXt block (conv -> LN -> Linear C->4C -> LN+SiLU -> Linear 4C->C + skip) on the
+    wide128 voxels, bf16: ms per block, effective TFLOP/s (valid-tap conv + both linears)."""
+    import torch
+
+    wl = pkg.workloads
+    coords = wl.make_coords("wide128_bf16")
+    n = coords.shape[0]
+    c, hid, dt = CONVNEXT_C, CONVNEXT_HIDDEN, torch.bfloat16
+    g = torch.Generator(device="cpu").manual_seed(7)
+
+    def rnd(*shape, scale=1.0):
+        return (torch.randn(*shape, generator=g) * scale).to(dev).to(dt)
+    x = pkg.SparseTensor(rnd(n, c), torch.from_numpy(coords).to(dev))
+    blk = pkg.SparseConvNeXtBlock3d(torch.from_numpy(wl.conv_weight(c, c, 3)).to(dev).to(dt),
+                                   rnd(c, scale=0.1), rnd(hid, c, scale=c ** -0.5),
+                                   rnd(hid, scale=0.1), rnd(c, hid, scale=hid ** -0.5),
+                                   rnd(c, scale=0.1))
+    nmap = pkg.get_neighbor_map(x)
+    nmap.conv_order()
+    p = int((nmap.nbr >= 0).sum().item())
+    ms = time_steps(lambda: blk(x), steps, warmup)
+    ctx = pkg._lib.context(dev.index)
+    kt = kernel_times(ctx, lambda: blk(x), 3)
+    flops_conv = 2.0 * p * c * c
+    flops_lin = 2.0 * 2 * n * c * hid
+    lin_ms = kt.get("linear", (0.0, 0))[0] * kt.get("linear", (0.0, 0))[1]
+    rec = {"workload": f"ConvNeXt block on wide128 ({n} voxels), C={c}, hidden={hid}, bf16",
+           "voxels": n, "ms_per_block": round(ms, 4),
+           "tflops_effective": round((flops_conv + flops_lin) / (ms / 1e3) / 1e12, 1),
+           "linear_tflops": round(flops_lin / (lin_ms / 1e3) / 1e12, 1) if lin_ms else None,
+           "bound": "mfma", "mfma_frac": round((flops_conv + flops_lin) / (ms / 1e3) / PEAK_MFMA["bfloat16"], 4),
+           "kernels": {k: {"avg_ms": round(a, 4), "launches_per_step": cnt} for k, (a, cnt) in kt.items()}}
+    log(f"convnext block: {ms:.4f} ms, {rec['tflops_effective']} TFLOP/s eff, "
+        f"linears {rec['linear_tflops']} TFLOP/s")
+    return rec
+
+
 def cpu_baseline(coords_np, shape, threads: int) -> dict:
     import torch
 
@@ -346,6 +388,7 @@ def main() -> int:
     if not args.no_secondary:
         sec = secondary(pkg, dev, args.steps, args.warmup, coords)
         sec += subdivide_records(pkg, dev, args.steps, args.warmup)
+        sec.append(convnext_record(pkg, dev, args.steps, args.warmup))
     cpu = None
     if not args.no_cpu_baseline:
         log(f"cpu baseline on {args.cpu_threads} threads ...")
