@@ -14,7 +14,8 @@ TFLOP/s counting only valid taps, algorithmic GB/s, roofline fraction):
   resblock64_bf16  4 x ResBlock (conv-LN-SiLU-conv-+x) at C=1024 bf16, 2 x ~32k voxels
 and the decoder upsample (tsc_subdivide) on the wide128 voxels with 512 bf16 channels, all 8
 children and a random keep mask (ms, algorithmic GB/s = coords + rows in and out, HBM fraction),
-and a sparse ConvNeXt block (conv + two linears, C=512, hidden 2048, bf16) on the same voxels.
+and a sparse ConvNeXt block (conv + two linears, C=512, hidden 2048, bf16) on the same voxels,
+and a 340 MB safetensors weight file streamed to the device (as stored, and widened to fp32).
 
 `roofline` is for the map build's dominant kernel, timed with hipEvents around each launch on
 the stream the library launches on; `cpu_baseline` times the PyTorch-CPU restatement of the
@@ -230,6 +231,66 @@ def convnext_record(pkg, dev, steps, warmup) -> dict:
     return rec
 
 
+ST_TENSORS, ST_C = 24, 512
+PEAK_HOST_LINK = 64e9  # B/s, PCIe 5.0 x16 host -> device, one direction
+
+
+def safetensors_record(pkg, steps) -> dict:
+    """Decoder-sized weight file (24 conv weights (512,3,3,3,512) bf16, 340 MB) streamed from a
+    file in the page cache to the device: as stored (bf16) and converted to fp32 on the GPU.
+    GB/s = file bytes / wall time of loading every tensor; the CPU leg is the reference's
+    readTensorF32 (host read + bf16 -> f32 widening) restated in numpy, on 4 of the tensors."""
+    import tempfile
+
+    import numpy as np
+    import torch
+    from safetensors.torch import save_file
+
+    from oracle import st_reader
+
+    wl = pkg.workloads
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "decoder.safetensors")
+        base = torch.from_numpy(wl.conv_weight(ST_C, ST_C, 9)).to(torch.bfloat16)
+        save_file({f"blocks.{i}.conv.weight": base.roll(i, 0).contiguous() for i in range(ST_TENSORS)},
+                  path)
+        nbytes = os.path.getsize(path)
+        res = {}
+        with pkg.SafetensorsFile(path, "cuda:0") as sf:
+            names = sf.list_tensors()
+            for label, dt in (("bf16 as stored", None), ("bf16 -> fp32 on the GPU", torch.float32)):
+                outs = []
+                for _ in range(2):  # warm-up (pinned staging, workspace, page cache)
+                    outs = [sf.read_tensor(n, dt) for n in names]
+                torch.cuda.synchronize()
+                del outs
+                times = []
+                for _ in range(max(3, steps // 4)):
+                    t0 = time.perf_counter()
+                    outs = [sf.read_tensor(n, dt) for n in names]
+                    torch.cuda.synchronize()
+                    times.append(time.perf_counter() - t0)
+                    del outs
+                t = statistics.median(times)
+                res[label] = {"ms": round(t * 1e3, 2), "gbps": round(nbytes / t / 1e9, 2),
+                              "host_link_frac": round(nbytes / t / PEAK_HOST_LINK, 4)}
+                log(f"safetensors load ({label}): {t * 1e3:.1f} ms, {nbytes / t / 1e9:.2f} GB/s")
+        sample = names[:4]
+        st_reader.read_f32(path, sample[0])
+        t0 = time.perf_counter()
+        for n in sample:
+            st_reader.read_f32(path, n)
+        tc = time.perf_counter() - t0
+        cpu_bytes = nbytes * len(sample) / len(names)
+    return {"workload": f"safetensors weight file: {ST_TENSORS} conv weights ({ST_C},3,3,3,{ST_C}) "
+                        f"bf16, {nbytes / 1e6:.0f} MB, page cache -> device",
+            "file_bytes": nbytes, "loads": res, "bound": "host link (PCIe 5.0 x16, 64 GB/s)",
+            "cpu_reference_reader": {"gbps": round(cpu_bytes / tc / 1e9, 2), "cores": 1,
+                                     "kind": "port",
+                                     "sample": f"{len(sample)} tensors, numpy read + bf16->f32 "
+                                               f"widening (readTensorF32)"}}
+
+
 def cpu_baseline(coords_np, shape, threads: int) -> dict:
     import torch
 
@@ -389,6 +450,7 @@ def main() -> int:
         sec = secondary(pkg, dev, args.steps, args.warmup, coords)
         sec += subdivide_records(pkg, dev, args.steps, args.warmup)
         sec.append(convnext_record(pkg, dev, args.steps, args.warmup))
+        sec.append(safetensors_record(pkg, args.steps))
     cpu = None
     if not args.no_cpu_baseline:
         log(f"cpu baseline on {args.cpu_threads} threads ...")

@@ -18,6 +18,8 @@
  *   decoder upsample (1 -> 8 children)                src/models/sparse_unet_vae_decoder.ts:155-175
  *   sparseLinear / ConvNeXt block linears             src/sparse/ops/linear.ts:9-29,
  *                                                     src/models/sparse_unet_vae_decoder.ts:48-78
+ *   SafetensorsFile + per-tensor upload               src/runtime/weights.ts:58-194,
+ *                                                     src/model/loader.ts:134-162
  */
 #ifndef TSC_H
 #define TSC_H
@@ -29,7 +31,7 @@
 extern "C" {
 #endif
 
-#define TSC_VERSION 2
+#define TSC_VERSION 3
 
 /* Status codes returned by every entry point. */
 enum tsc_status {
@@ -176,6 +178,50 @@ int tsc_linear(tsc_ctx* ctx, int32_t dtype, const void* x, int64_t N, int32_t Ci
 int tsc_subdivide_count(tsc_ctx* ctx, const uint8_t* keep, int64_t N, int64_t* count);
 int tsc_subdivide(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t dtype, const void* feats,
                   int32_t C, const uint8_t* keep, int32_t* coords_out, void* feats_out);
+
+/* ---- safetensors weight files -------------------------------------------------------------- */
+/* Element types of a safetensors header ("dtype" strings).  F32/F16/BF16 equal TSC_F32/F16/BF16. */
+enum tsc_st_dtype {
+  TSC_ST_F32 = 0, TSC_ST_F16 = 1, TSC_ST_BF16 = 2, TSC_ST_F64 = 3, TSC_ST_I64 = 4, TSC_ST_I32 = 5,
+  TSC_ST_I16 = 6, TSC_ST_I8 = 7, TSC_ST_U8 = 8, TSC_ST_BOOL = 9, TSC_ST_U16 = 10, TSC_ST_U32 = 11,
+  TSC_ST_U64 = 12, TSC_ST_F8_E4M3 = 13, TSC_ST_F8_E5M2 = 14
+};
+/* out_dtype of tsc_st_load that copies the stored bytes unchanged. */
+#define TSC_ST_RAW (-1)
+
+typedef struct tsc_st tsc_st;
+/* Opens a .safetensors file and parses its header only (8-byte little-endian length + JSON);
+ * tensor data stays on disk until loaded.  Rejects malformed headers, unknown dtypes, duplicate
+ * names and data offsets that disagree with shape x dtype or lie outside the file.
+ * Replaces SafetensorsFile.open (src/runtime/weights.ts:67-99). */
+int tsc_st_open(const char* path, tsc_st** out);
+int tsc_st_close(tsc_st* f);                                       /* weights.ts:188-192 */
+/* Number of tensors and of __metadata__ entries, and the file offset of the data block
+ * (SafetensorsHeader.tensors.size / metadata / dataByteOffset, weights.ts:18-22, 106-108). */
+int tsc_st_counts(tsc_st* f, int64_t* tensors, int64_t* metadata, int64_t* data_offset);
+/* Name of tensor `index` in header order, NUL-terminated into name[name_len]
+ * (listTensors, weights.ts:111-113). */
+int tsc_st_name(tsc_st* f, int64_t index, char* name, int32_t name_len);
+/* Metadata entry `index` (header order) as NUL-terminated key and value (weights.ts:94). */
+int tsc_st_metadata(tsc_st* f, int64_t index, char* key, int32_t key_len, char* value,
+                    int32_t value_len);
+/* dtype (tsc_st_dtype), rank, shape (up to max_dims entries) and data_offsets [begin, end)
+ * relative to the data block of a tensor; any output may be NULL (getTensorInfo,
+ * weights.ts:120-123).  Unknown names are TSC_ERR_INVALID. */
+int tsc_st_info(tsc_st* f, const char* name, int32_t* dtype, int32_t* ndim, int64_t* shape,
+                int32_t max_dims, int64_t* offsets);
+/* Streams one tensor from the file into device memory dst on the context's stream.
+ *   out_dtype TSC_ST_RAW (or the stored float type): the stored bytes unchanged (readTensorRaw,
+ *             weights.ts:125-142); dst holds end - begin bytes.
+ *   out_dtype TSC_F32 / TSC_F16 / TSC_BF16 from a stored F32, F16 or BF16 tensor: converted on the
+ *             GPU, numel elements of out_dtype.  To F32 this is readTensorF32 bit for bit
+ *             (weights.ts:150-177: BF16 bits << 16; F16 IEEE widening, NaN -> sign|0x7fc00000);
+ *             to F16/BF16 round to nearest even, NaN -> sign | canonical quiet NaN.
+ *             Other stored types must be loaded raw (TSC_ERR_UNSUPPORTED).
+ * Returns once the last chunk is queued: work later on the same stream sees the tensor; the host
+ * waits with tsc_sync.  Replaces the per-tensor upload of loadModelWeights
+ * (src/model/loader.ts:134-162, getTensor). */
+int tsc_st_load(tsc_ctx* ctx, tsc_st* f, const char* name, int32_t out_dtype, void* dst);
 
 /* ---- per-kernel timing -------------------------------------------------------------------- */
 /* While enabled, every kernel the context launches is bracketed by hipEvents on its stream.

@@ -9,6 +9,7 @@ is not a Python identifier.
   SparseSubdivide, sparse_subdivide              decoder upsample (sparse_unet_vae_decoder.ts:155-175)
   SparseLinear, SparseConvNeXtBlock3d,           decoder blocks (linear.ts:9-29,
   sparse_linear                                  sparse_unet_vae_decoder.ts:48-78)
+  SafetensorsFile, MultiFileLoader               weight files -> device tensors (weights.ts:58-237)
   workloads                                      seeded synthetic voxel shells
 """
 from ._lib import TscError, load_library, header_symbols, LIB_PATH  # noqa: F401
@@ -19,12 +20,13 @@ from .ops import (NeighborMap, build_neighbor_map, map_conv_order, sparse_conv3d
                   sparse_linear)
 from .spatial import SparseSubdivide  # noqa: F401
 from .blocks import SparseLinear, SparseConvNeXtBlock3d  # noqa: F401
+from .weights import SafetensorsFile, SafetensorsHeader, TensorEntry, MultiFileLoader  # noqa: F401
 from . import workloads  # noqa: F401
 
 __all__ = [
     "TscError", "SparseTensor", "SparseConv3d", "SparseResBlock3d", "NeighborMap",
     "build_neighbor_map", "map_conv_order", "sparse_conv3d", "layer_norm", "silu", "add", "sparse_resblock",
     "sparse_subdivide", "subdivide_count", "SparseSubdivide", "sparse_linear", "SparseLinear",
-    "SparseConvNeXtBlock3d",
+    "SparseConvNeXtBlock3d", "SafetensorsFile", "SafetensorsHeader", "TensorEntry", "MultiFileLoader",
     "get_neighbor_map", "neighbor_cache_key", "workloads",
 ]

@@ -19,6 +19,11 @@ TSC_F32, TSC_F16, TSC_BF16 = 0, 1, 2
 TSC_MAP_DUPLICATE, TSC_MAP_OUT_OF_RANGE = 1, 2
 TSC_MAP_AUTO, TSC_MAP_BITMAP, TSC_MAP_RADIX = 0, 1, 2
 TSC_EPI_BIAS, TSC_EPI_BIAS_RESIDUAL, TSC_EPI_BIAS_LN_SILU = 0, 1, 2
+TSC_ST_RAW = -1
+# safetensors header dtype strings in tsc_st_dtype order, with their element sizes
+ST_DTYPES = ("F32", "F16", "BF16", "F64", "I64", "I32", "I16", "I8", "U8", "BOOL", "U16", "U32",
+             "U64", "F8_E4M3", "F8_E5M2")
+ST_SIZES = (4, 2, 2, 8, 8, 4, 2, 1, 1, 1, 2, 4, 8, 1, 1)
 
 MAP_METHODS = {"auto": TSC_MAP_AUTO, "bitmap": TSC_MAP_BITMAP, "radix": TSC_MAP_RADIX}
 
@@ -66,6 +71,14 @@ _SIGNATURES = {
     "tsc_linear": (_I32, [_P, _I32, _P, _I64, _I32, _P, _P, _P, _I32, _P]),
     "tsc_subdivide_count": (_I32, [_P, _P, _I64, ctypes.POINTER(_I64)]),
     "tsc_subdivide": (_I32, [_P, _P, _I64, _I32, _P, _I32, _P, _P, _P]),
+    "tsc_st_open": (_I32, [ctypes.c_char_p, ctypes.POINTER(_P)]),
+    "tsc_st_close": (_I32, [_P]),
+    "tsc_st_counts": (_I32, [_P, ctypes.POINTER(_I64), ctypes.POINTER(_I64), ctypes.POINTER(_I64)]),
+    "tsc_st_name": (_I32, [_P, _I64, ctypes.c_char_p, _I32]),
+    "tsc_st_metadata": (_I32, [_P, _I64, ctypes.c_char_p, _I32, ctypes.c_char_p, _I32]),
+    "tsc_st_info": (_I32, [_P, ctypes.c_char_p, ctypes.POINTER(_I32), ctypes.POINTER(_I32),
+                           ctypes.POINTER(_I64), _I32, ctypes.POINTER(_I64)]),
+    "tsc_st_load": (_I32, [_P, _P, ctypes.c_char_p, _I32, _P]),
     "tsc_profile_enable": (_I32, [_P, _I32]),
     "tsc_profile_collect": (_I32, [_P, ctypes.POINTER(_I32)]),
     "tsc_profile_entry": (_I32, [_P, _I32, ctypes.c_char_p, _I32, ctypes.POINTER(ctypes.c_double),

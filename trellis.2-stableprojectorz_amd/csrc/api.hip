@@ -168,6 +168,7 @@ int tsc_ctx_destroy(tsc_ctx* ctx) {
   if (ctx->ws_sched) (void)hipFree(ctx->ws_sched);
   blas_destroy(ctx);
   if (ctx->ws_blas) (void)hipFree(ctx->ws_blas);
+  st_release(ctx);
   prof_clear(ctx);
   delete ctx;
   return st;
@@ -453,6 +454,55 @@ int tsc_subdivide(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t dtype,
   }
   DeviceGuard g(ctx->device);
   return subdivide_launch(ctx, coords, N, feats, row_bytes, keep, coords_out, feats_out);
+}
+
+int tsc_st_open(const char* path, tsc_st** out) {
+  g_err[0] = 0;
+  if (!path || !out) return fail(TSC_ERR_INVALID, "st_open: null argument");
+  *out = nullptr;
+  return st_open(path, out);
+}
+
+int tsc_st_close(tsc_st* f) {
+  g_err[0] = 0;
+  if (f) st_close(f);
+  return TSC_OK;
+}
+
+int tsc_st_counts(tsc_st* f, int64_t* tensors, int64_t* metadata, int64_t* data_offset) {
+  g_err[0] = 0;
+  if (!f) return fail(TSC_ERR_INVALID, "st_counts: null file");
+  st_counts(f, tensors, metadata, data_offset);
+  return TSC_OK;
+}
+
+int tsc_st_name(tsc_st* f, int64_t index, char* name, int32_t name_len) {
+  g_err[0] = 0;
+  if (!f) return fail(TSC_ERR_INVALID, "st_name: null file");
+  return st_name(f, index, name, name_len);
+}
+
+int tsc_st_metadata(tsc_st* f, int64_t index, char* key, int32_t key_len, char* value,
+                    int32_t value_len) {
+  g_err[0] = 0;
+  if (!f) return fail(TSC_ERR_INVALID, "st_metadata: null file");
+  return st_metadata(f, index, key, key_len, value, value_len);
+}
+
+int tsc_st_info(tsc_st* f, const char* name, int32_t* dtype, int32_t* ndim, int64_t* shape,
+                int32_t max_dims, int64_t* offsets) {
+  g_err[0] = 0;
+  if (!f || !name) return fail(TSC_ERR_INVALID, "st_info: null argument");
+  return st_info(f, name, dtype, ndim, shape, max_dims, offsets);
+}
+
+int tsc_st_load(tsc_ctx* ctx, tsc_st* f, const char* name, int32_t out_dtype, void* dst) {
+  g_err[0] = 0;
+  int st = check_ctx(ctx);
+  if (st) return st;
+  if (!f || !name) return fail(TSC_ERR_INVALID, "st_load: null argument");
+  DeviceGuard g(ctx->device);
+  return st_load(ctx, f, name, out_dtype, dst);
 }
 
 int tsc_profile_enable(tsc_ctx* ctx, int on) {

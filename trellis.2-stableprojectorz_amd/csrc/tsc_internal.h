@@ -35,6 +35,11 @@ struct tsc_ctx {
   void* blaslt = nullptr;
   void* ws_blas = nullptr;
   size_t ws_blas_bytes = 0;
+  // Pinned host chunks (and their last copies' events) of the safetensors reader.
+  void* st_pin[2] = {nullptr, nullptr};
+  hipEvent_t st_ev[2] = {nullptr, nullptr};
+  bool st_pending[2] = {false, false};
+  int st_next = 0;  // chunk the next load starts with
   bool profile = false;
   std::vector<tsc_prof_rec> prof;      // pending launches
   std::vector<tsc_prof_agg> prof_agg;  // aggregated by tsc_profile_collect
@@ -123,6 +128,18 @@ int linear_launch(tsc_ctx* ctx, int32_t dtype, const void* x, int64_t N, int32_t
                   const void* weight, const void* bias, const void* residual, int32_t Cout,
                   void* out);
 void blas_destroy(tsc_ctx* ctx);
+
+// ---- implemented in safetensors.hip ----
+int st_open(const char* path, tsc_st** out);
+void st_close(tsc_st* f);
+void st_counts(const tsc_st* f, int64_t* tensors, int64_t* metadata, int64_t* data_offset);
+int st_name(const tsc_st* f, int64_t i, char* buf, int32_t len);
+int st_metadata(const tsc_st* f, int64_t i, char* key, int32_t key_len, char* value,
+                int32_t value_len);
+int st_info(const tsc_st* f, const char* name, int32_t* dtype, int32_t* ndim, int64_t* shape,
+            int32_t max_dims, int64_t* offsets);
+int st_load(tsc_ctx* ctx, const tsc_st* f, const char* name, int32_t out_dtype, void* dst);
+void st_release(tsc_ctx* ctx);
 
 // ---- launchers implemented in rowops.hip ----
 int layernorm_launch(tsc_ctx* ctx, int32_t dtype, const void* x, int64_t N, int32_t C,
