@@ -15,6 +15,8 @@ Contents
                     children, optional keep mask)
   linear(), convnext_block()
                     fp64 numpy restatements of nn.Linear per voxel and the sparse ConvNeXt block
+  st_reader.py      numpy restatement of the reference's safetensors reader and its float
+                    conversions (pinned in its own docstring and tests/test_safetensors.py)
 
 Pinning (see tests/test_oracle.py): the map builds are checked against each other and against
 brute force, sorted keys against numpy.unique, the conv against a dense torch F.conv3d closed
