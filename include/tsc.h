@@ -18,6 +18,8 @@
  *   decoder upsample (1 -> 8 children)                src/models/sparse_unet_vae_decoder.ts:155-175
  *   sparseLinear / ConvNeXt block linears             src/sparse/ops/linear.ts:9-29,
  *                                                     src/models/sparse_unet_vae_decoder.ts:48-78
+ *   sparseAttention / scaledDotProductAttention       src/sparse/ops/attention.ts:24-79,
+ *                                                     src/dense/ops/attention.ts:36-110
  *   SafetensorsFile + per-tensor upload               src/runtime/weights.ts:58-194,
  *                                                     src/model/loader.ts:134-162
  */
@@ -31,7 +33,7 @@
 extern "C" {
 #endif
 
-#define TSC_VERSION 3
+#define TSC_VERSION 4
 
 /* Status codes returned by every entry point. */
 enum tsc_status {
@@ -178,6 +180,26 @@ int tsc_linear(tsc_ctx* ctx, int32_t dtype, const void* x, int64_t N, int32_t Ci
 int tsc_subdivide_count(tsc_ctx* ctx, const uint8_t* keep, int64_t N, int64_t* count);
 int tsc_subdivide(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t dtype, const void* feats,
                   int32_t C, const uint8_t* keep, int32_t* coords_out, void* feats_out);
+
+/* ---- varlen attention ---------------------------------------------------------------------- */
+/* Scaled-dot-product attention over packed variable-length sequences:
+ *   out[n,h,:] = softmax_m(q[n,h,:] . k[m,h,:] * scale) v[m,h,:]
+ * for n in [cu_seqlens_q[b], cu_seqlens_q[b+1]) and m in [cu_seqlens_kv[b], cu_seqlens_kv[b+1]),
+ * b < B.  A sequence with no keys gives zeros.
+ *   q, out (total_q, num_heads, head_dim), k, v (total_kv, num_heads, head_dim): `dtype`,
+ *     row-major, 16-byte aligned; out must not alias an input.  head_dim 64 or 128.
+ *   cu_seqlens_q / cu_seqlens_kv  device int32 (B+1), non-decreasing, within [0, total]
+ *     (values outside are clamped, so a malformed array cannot read out of bounds).
+ *   scale  <= 0 means 1/sqrt(head_dim) (attention.ts:64).  max_seqlen_q sizes the grid (longer
+ *     sequences are still covered, at a lower parallelism).
+ * bf16/f16 on v_mfma 32x32x16 with fp32 softmax and accumulation (P rounded to the input type
+ * for the second product); f32 on v_mfma 32x32x2f32.
+ * Replaces sparseAttention (src/sparse/ops/attention.ts:24-79: B > 1 as a per-sample CPU round
+ * trip) and, with B = 1, scaledDotProductAttention (src/dense/ops/attention.ts:36-110). */
+int tsc_attention(tsc_ctx* ctx, int32_t dtype, const void* q, const void* k, const void* v,
+                  const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_kv, int32_t B,
+                  int64_t total_q, int64_t total_kv, int32_t num_heads, int32_t head_dim,
+                  float scale, int32_t max_seqlen_q, void* out);
 
 /* ---- safetensors weight files -------------------------------------------------------------- */
 /* Element types of a safetensors header ("dtype" strings).  F32/F16/BF16 equal TSC_F32/F16/BF16. */

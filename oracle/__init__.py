@@ -15,6 +15,7 @@ Contents
                     children, optional keep mask)
   linear(), convnext_block()
                     fp64 numpy restatements of nn.Linear per voxel and the sparse ConvNeXt block
+  attention()       fp64 numpy restatement of varlen scaled-dot-product attention
   st_reader.py      numpy restatement of the reference's safetensors reader and its float
                     conversions (pinned in its own docstring and tests/test_safetensors.py)
 
@@ -29,6 +30,10 @@ subdivision equals the union of eight single-child keep masks.  The reference ho
 fixtures for it (its TS port does not generate children: sparse_unet_vae_decoder.ts:155-175);
 the child order follows torch.nonzero over a 2x2x2 cube (dx slowest, dz fastest), the order of
 trellis2's SparseSubdivide, which is not in this container: that convention is parity unpinned.
+attention() is pinned against torch.nn.functional.scaled_dot_product_attention in fp64 per
+sequence, and by closed forms: constant V rows give that row, zero queries give the mean of V,
+one key gives its V row, a key permutation leaves the output unchanged, and a sequence without
+keys gives zeros (attention.ts:57).
 linear() is pinned against torch.nn.functional.linear in fp64; convnext_block() is the
 composition of the pinned conv, layernorm and linear (the block's step order is the TS port's,
 sparse_unet_vae_decoder.ts:48-78).
@@ -215,3 +220,32 @@ def convnext_block(feats, nbr, conv_w, conv_b, w0, b0, w2, b2, eps=1e-6, rows=No
     h = layernorm(h, None, None, eps, silu=True)
     skip = f if rows is None else f[rows]
     return linear(h, w2, b2, skip)
+
+
+def attention(q, k, v, cu_q, cu_kv, scale=None, rows=None) -> np.ndarray:
+    """Varlen scaled-dot-product attention in fp64 (src/sparse/ops/attention.ts:24-79: per
+    sequence b, softmax(Q_b K_b^T * scale) V_b per head; a sequence without keys stays zero,
+    :57).  q (total_q, H, D), k / v (total_kv, H, D); `rows` restricts the output to those query
+    rows (the others are zero)."""
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    d = q.shape[-1]
+    scale = 1.0 / np.sqrt(d) if scale is None else scale
+    out = np.zeros(q.shape, np.float64)
+    want = None if rows is None else np.zeros(q.shape[0], bool)
+    if want is not None:
+        want[np.asarray(rows)] = True
+    for b in range(len(cu_q) - 1):
+        q0, q1, k0, k1 = int(cu_q[b]), int(cu_q[b + 1]), int(cu_kv[b]), int(cu_kv[b + 1])
+        if q1 <= q0 or k1 <= k0:
+            continue
+        idx = np.arange(q0, q1) if want is None else np.nonzero(want[q0:q1])[0] + q0
+        if idx.size == 0:
+            continue
+        s = np.einsum("nhd,mhd->hnm", q[idx], k[k0:k1]) * scale
+        s -= s.max(axis=-1, keepdims=True)
+        p = np.exp(s)
+        p /= p.sum(axis=-1, keepdims=True)
+        out[idx] = np.einsum("hnm,mhd->nhd", p, v[k0:k1])
+    return out

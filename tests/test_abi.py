@@ -11,7 +11,7 @@ def test_library_exports_every_declared_symbol(pkg):
     assert len(declared) >= 18
     missing = [s for s in declared if not hasattr(lib, s)]
     assert not missing, missing
-    assert lib.tsc_version() == 3
+    assert lib.tsc_version() == 4
 
 
 def test_null_context_and_bad_arguments_fail_cleanly(pkg):

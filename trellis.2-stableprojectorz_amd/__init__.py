@@ -9,6 +9,8 @@ is not a Python identifier.
   SparseSubdivide, sparse_subdivide              decoder upsample (sparse_unet_vae_decoder.ts:155-175)
   SparseLinear, SparseConvNeXtBlock3d,           decoder blocks (linear.ts:9-29,
   sparse_linear                                  sparse_unet_vae_decoder.ts:48-78)
+  sparse_attention,                              varlen attention (sparse/ops/attention.ts:24-79,
+  scaled_dot_product_attention                   dense/ops/attention.ts:36-110)
   SafetensorsFile, MultiFileLoader               weight files -> device tensors (weights.ts:58-237)
   workloads                                      seeded synthetic voxel shells
 """
@@ -17,7 +19,7 @@ from .sparse_tensor import SparseTensor, Scale, Fraction, SCALE_IDENTITY, comput
 from .conv3d import SparseConv3d, SparseResBlock3d, get_neighbor_map, neighbor_cache_key  # noqa: F401
 from .ops import (NeighborMap, build_neighbor_map, map_conv_order, sparse_conv3d,  # noqa: F401
                   layer_norm, silu, add, sparse_resblock, sparse_subdivide, subdivide_count,
-                  sparse_linear)
+                  sparse_linear, sparse_attention, scaled_dot_product_attention)
 from .spatial import SparseSubdivide  # noqa: F401
 from .blocks import SparseLinear, SparseConvNeXtBlock3d  # noqa: F401
 from .weights import SafetensorsFile, SafetensorsHeader, TensorEntry, MultiFileLoader  # noqa: F401
@@ -27,6 +29,6 @@ __all__ = [
     "TscError", "SparseTensor", "SparseConv3d", "SparseResBlock3d", "NeighborMap",
     "build_neighbor_map", "map_conv_order", "sparse_conv3d", "layer_norm", "silu", "add", "sparse_resblock",
     "sparse_subdivide", "subdivide_count", "SparseSubdivide", "sparse_linear", "SparseLinear",
-    "SparseConvNeXtBlock3d", "SafetensorsFile", "SafetensorsHeader", "TensorEntry", "MultiFileLoader",
+    "SparseConvNeXtBlock3d", "sparse_attention", "scaled_dot_product_attention", "SafetensorsFile", "SafetensorsHeader", "TensorEntry", "MultiFileLoader",
     "get_neighbor_map", "neighbor_cache_key", "workloads",
 ]

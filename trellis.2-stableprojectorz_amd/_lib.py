@@ -71,6 +71,8 @@ _SIGNATURES = {
     "tsc_linear": (_I32, [_P, _I32, _P, _I64, _I32, _P, _P, _P, _I32, _P]),
     "tsc_subdivide_count": (_I32, [_P, _P, _I64, ctypes.POINTER(_I64)]),
     "tsc_subdivide": (_I32, [_P, _P, _I64, _I32, _P, _I32, _P, _P, _P]),
+    "tsc_attention": (_I32, [_P, _I32, _P, _P, _P, _P, _P, _I32, _I64, _I64, _I32, _I32, _F32,
+                             _I32, _P]),
     "tsc_st_open": (_I32, [ctypes.c_char_p, ctypes.POINTER(_P)]),
     "tsc_st_close": (_I32, [_P]),
     "tsc_st_counts": (_I32, [_P, ctypes.POINTER(_I64), ctypes.POINTER(_I64), ctypes.POINTER(_I64)]),

@@ -3,6 +3,7 @@
 // GPU input, Ci = weight.shape[4], Co = weight.shape[0]) and adds the checks a C ABI needs
 // (null pointers, alignment, size limits), so bad input becomes a status code, never a fault.
 
+#include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
@@ -454,6 +455,33 @@ int tsc_subdivide(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t dtype,
   }
   DeviceGuard g(ctx->device);
   return subdivide_launch(ctx, coords, N, feats, row_bytes, keep, coords_out, feats_out);
+}
+
+int tsc_attention(tsc_ctx* ctx, int32_t dtype, const void* q, const void* k, const void* v,
+                  const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_kv, int32_t B,
+                  int64_t total_q, int64_t total_kv, int32_t num_heads, int32_t head_dim,
+                  float scale, int32_t max_seqlen_q, void* out) {
+  g_err[0] = 0;
+  int st = check_ctx(ctx);
+  if (st) return st;
+  if (!elem_size(dtype)) return fail(TSC_ERR_INVALID, "attention: unknown dtype %d", dtype);
+  if (head_dim != 64 && head_dim != 128)
+    return fail(TSC_ERR_UNSUPPORTED, "attention: head_dim %d (64 and 128 are supported)", head_dim);
+  if (B < 0 || num_heads <= 0 || num_heads > 65535 || B > 65535 || total_q < 0 || total_kv < 0 ||
+      max_seqlen_q < 0 || total_q > INT32_MAX || total_kv > INT32_MAX)
+    return fail(TSC_ERR_INVALID, "attention: bad sizes B=%d H=%d total_q=%lld total_kv=%lld", B,
+                num_heads, (long long)total_q, (long long)total_kv);
+  if (B == 0 || total_q == 0) return TSC_OK;
+  if (!q || !out || !cu_seqlens_q || !cu_seqlens_kv || (total_kv > 0 && (!k || !v)))
+    return fail(TSC_ERR_INVALID, "attention: null buffer");
+  if (!aligned(q, 16) || !aligned(out, 16) || (total_kv > 0 && (!aligned(k, 16) || !aligned(v, 16))))
+    return fail(TSC_ERR_INVALID, "attention: q, k, v and out must be 16-byte aligned");
+  if (out == q || out == k || out == v) return fail(TSC_ERR_INVALID, "attention: out aliases an input");
+  if (!(scale > 0.f)) scale = 1.f / sqrtf((float)head_dim);
+  DeviceGuard g(ctx->device);
+  return attention_launch(ctx, dtype, q, total_kv > 0 ? k : q, total_kv > 0 ? v : q, cu_seqlens_q,
+                          cu_seqlens_kv, B, total_q, total_kv, num_heads, head_dim, scale,
+                          max_seqlen_q, out);
 }
 
 int tsc_st_open(const char* path, tsc_st** out) {

@@ -141,6 +141,12 @@ int st_info(const tsc_st* f, const char* name, int32_t* dtype, int32_t* ndim, in
 int st_load(tsc_ctx* ctx, const tsc_st* f, const char* name, int32_t out_dtype, void* dst);
 void st_release(tsc_ctx* ctx);
 
+// ---- implemented in attention.hip ----
+int attention_launch(tsc_ctx* ctx, int32_t dtype, const void* q, const void* k, const void* v,
+                     const int32_t* cu_q, const int32_t* cu_kv, int32_t B, int64_t total_q,
+                     int64_t total_kv, int32_t H, int32_t D, float scale, int32_t max_seqlen_q,
+                     void* out);
+
 // ---- launchers implemented in rowops.hip ----
 int layernorm_launch(tsc_ctx* ctx, int32_t dtype, const void* x, int64_t N, int32_t C,
                      const void* gamma, const void* beta, float eps, int32_t apply_silu, void* y);

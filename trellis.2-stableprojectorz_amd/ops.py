@@ -270,3 +270,78 @@ def sparse_linear(x: torch.Tensor, weight: torch.Tensor, bias=None, residual=Non
     check(ctx.lib.tsc_linear(ctx.bind(), _code(x), _p(x), n, cin, _p(weight), _p(bias),
                              _p(residual), cout, _p(out)))
     return out
+
+
+def _cu_seqlens(cu, total: int, dev: int, what: str):
+    """cu_seqlens as (host int64 array, device int32 tensor), checked non-decreasing in [0, total]."""
+    import numpy as np
+
+    if isinstance(cu, torch.Tensor):
+        host = cu.detach().to("cpu", torch.int64).numpy()
+    else:
+        host = np.asarray(cu, np.int64)
+    if host.ndim != 1 or host.size < 1:
+        raise TscError(_lib.TSC_ERR_INVALID, f"{what} must be a 1-D (B+1,) sequence")
+    if (np.diff(host) < 0).any() or host[0] < 0 or host[-1] > total:
+        raise TscError(_lib.TSC_ERR_INVALID, f"{what} must be non-decreasing within [0, {total}]")
+    if isinstance(cu, torch.Tensor) and cu.is_cuda and cu.dtype == torch.int32 and cu.is_contiguous():
+        d = cu
+    else:
+        d = torch.from_numpy(host.astype(np.int32)).to(f"cuda:{dev}")
+    return host, d
+
+
+def sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens_q,
+                     cu_seqlens_kv=None, num_heads: int | None = None, head_dim: int | None = None,
+                     scale: float | None = None, out=None) -> torch.Tensor:
+    """sparseAttention (src/sparse/ops/attention.ts:24-79) on the GPU for any batch size.
+
+    q (total_q, H, D) and k / v (total_kv, H, D), or (total, H*D) with num_heads; cu_seqlens_q /
+    cu_seqlens_kv (B+1,) row offsets of each sequence (host sequence or tensor; cu_seqlens_kv
+    defaults to cu_seqlens_q).  Returns (total_q, H, D) in q's dtype.  scale defaults to
+    1/sqrt(D).  One tsc_attention call; no host round trip."""
+    dev = _dev(q, k, v, out)
+    if q.dim() == 2:
+        if not num_heads:
+            raise TscError(_lib.TSC_ERR_INVALID, "num_heads is required for (total, H*D) inputs")
+        h = num_heads
+        d = q.shape[1] // h
+    else:
+        h, d = q.shape[1], q.shape[2]
+    if num_heads is not None and num_heads != h or head_dim is not None and head_dim != d:
+        raise TscError(_lib.TSC_ERR_INVALID, f"num_heads/head_dim {num_heads}/{head_dim} do not "
+                                             f"match the query shape {tuple(q.shape)}")
+    tq, tkv = q.shape[0], k.shape[0]
+    for name, t, n in (("q", q, tq), ("k", k, tkv), ("v", v, tkv)):
+        if t.numel() != n * h * d or t.dtype != q.dtype:
+            raise TscError(_lib.TSC_ERR_INVALID, f"{name} must hold ({n}, {h}, {d}) {q.dtype} values")
+    cq_host, cq = _cu_seqlens(cu_seqlens_q, tq, dev, "cu_seqlens_q")
+    if cu_seqlens_kv is None:
+        cu_seqlens_kv = cu_seqlens_q
+    ck_host, ck = _cu_seqlens(cu_seqlens_kv, tkv, dev, "cu_seqlens_kv")
+    if len(ck_host) != len(cq_host):
+        raise TscError(_lib.TSC_ERR_INVALID, "cu_seqlens_q and cu_seqlens_kv differ in length")
+    b = len(cq_host) - 1
+    if out is None:
+        out = torch.empty((tq, h, d), dtype=q.dtype, device=q.device)
+    elif out.numel() != tq * h * d or out.dtype != q.dtype:
+        raise TscError(_lib.TSC_ERR_INVALID, "out has the wrong size or dtype")
+    max_q = int((cq_host[1:] - cq_host[:-1]).max()) if b > 0 else 0
+    ctx = _lib.context(dev)
+    check(ctx.lib.tsc_attention(ctx.bind(), _code(q), _p(q), _p(k), _p(v), _p(cq), _p(ck), b, tq,
+                                tkv, h, d, float(scale) if scale else 0.0, max_q, _p(out)))
+    return out.view(tq, h, d)
+
+
+def scaled_dot_product_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                                 num_heads: int, batch_size: int = 1, scale=None) -> torch.Tensor:
+    """scaledDotProductAttention (src/dense/ops/attention.ts:36-110): q (B*S_q, H, D) or
+    (B, S_q, H, D), k / v likewise with S_kv; batch_size equal-length sequences."""
+    sq = q.numel() // (batch_size * q.shape[-1] * num_heads)
+    skv = k.numel() // (batch_size * k.shape[-1] * num_heads)
+    d = q.shape[-1]
+    cq = [i * sq for i in range(batch_size + 1)]
+    ck = [i * skv for i in range(batch_size + 1)]
+    o = sparse_attention(q.reshape(-1, num_heads, d), k.reshape(-1, num_heads, d),
+                         v.reshape(-1, num_heads, d), cq, ck, scale=scale)
+    return o.view(q.shape)
