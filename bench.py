@@ -15,7 +15,9 @@ TFLOP/s counting only valid taps, algorithmic GB/s, roofline fraction):
 and the decoder upsample (tsc_subdivide) on the wide128 voxels with 512 bf16 channels, all 8
 children and a random keep mask (ms, algorithmic GB/s = coords + rows in and out, HBM fraction),
 and a sparse ConvNeXt block (conv + two linears, C=512, hidden 2048, bf16) on the same voxels,
-and a 340 MB safetensors weight file streamed to the device (as stored, and widened to fp32).
+varlen self-attention over the resblock64 voxels (12 heads x 128, bf16 and fp32: TFLOP/s, MFMA
+fraction), and a 340 MB safetensors weight file streamed to the device (as stored, and widened to
+fp32).
 
 `roofline` is for the map build's dominant kernel, timed with hipEvents around each launch on
 the stream the library launches on; `cpu_baseline` times the PyTorch-CPU restatement of the
@@ -229,6 +231,65 @@ def convnext_record(pkg, dev, steps, warmup) -> dict:
     log(f"convnext block: {ms:.4f} ms, {rec['tflops_effective']} TFLOP/s eff, "
         f"linears {rec['linear_tflops']} TFLOP/s")
     return rec
+
+
+ATTN_HEADS, ATTN_DIM = 12, 128  # SLat flow transformer: 1536 channels, 12 heads
+
+
+def attention_record(pkg, dev, steps) -> dict:
+    """Varlen self-attention over the voxels of the resblock64 shells (2 sequences, one per
+    sample), 12 heads x 128, as the SLat flow's blocks run it: ms per call, TFLOP/s (4*D flops per
+    query-key pair and head), MFMA fraction; bf16 and fp32.  The CPU leg is the same attention in
+    numpy fp32 (BLAS) on one head of 2048 queries against all keys of sample 0."""
+    import numpy as np
+    import torch
+
+    wl = pkg.workloads
+    coords = wl.make_coords("resblock64_bf16")
+    counts = np.bincount(coords[:, 0])
+    cu = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+    n, h, d = int(cu[-1]), ATTN_HEADS, ATTN_DIM
+    pairs = float((counts.astype(np.float64) ** 2).sum())
+    flops = 4.0 * h * d * pairs
+    g = torch.Generator(device="cpu").manual_seed(11)
+    out = {"workload": f"varlen self-attention over the resblock64 voxels ({len(counts)} sequences, "
+                       f"{n} tokens), {h} heads x {d}",
+           "tokens": n, "sequences": [int(c) for c in counts], "flops_per_call": flops}
+    ctx = pkg._lib.context(dev.index)
+    for dt, name in ((torch.bfloat16, "bfloat16"), (torch.float32, "float32")):
+        q, k, v = (torch.randn((n, h, d), generator=g).to(dev).to(dt) for _ in range(3))
+        cu_d = torch.from_numpy(cu.astype(np.int32)).to(dev)
+        o = torch.empty_like(q)
+
+        def run():
+            return pkg.sparse_attention(q, k, v, cu_d, out=o)
+        reps = steps if dt == torch.bfloat16 else max(2, steps // 8)
+        ms = time_steps(run, reps, 2)
+        kt = kernel_times(ctx, run, 2)
+        tf = flops / (ms / 1e3)
+        out[name] = {"ms": round(ms, 3), "tflops": round(tf / 1e12, 1),
+                     "mfma_frac": round(tf / PEAK_MFMA[name], 4),
+                     "kernels": {kk: {"avg_ms": round(a, 4), "launches_per_step": c}
+                                 for kk, (a, c) in kt.items()}}
+        log(f"attention {name}: {ms:.3f} ms, {tf / 1e12:.1f} TFLOP/s, "
+            f"{tf / PEAK_MFMA[name]:.3f} of MFMA peak")
+        del q, k, v, o
+        torch.cuda.empty_cache()
+    rng = np.random.default_rng(0)
+    nq, nk = 2048, int(counts[0])
+    qh, kh, vh = (rng.standard_normal((m, d)).astype(np.float32) for m in (nq, nk, nk))
+    t0 = time.perf_counter()
+    s = qh @ kh.T * np.float32(d ** -0.5)
+    s -= s.max(axis=1, keepdims=True)
+    np.exp(s, out=s)
+    s /= s.sum(axis=1, keepdims=True)
+    _ = s @ vh
+    tc = time.perf_counter() - t0
+    out["cpu_numpy_fp32"] = {"tflops": round(4.0 * d * nq * nk / tc / 1e12, 4),
+                             "cores": int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)),
+                             "kind": "port",
+                             "sample": f"1 head, {nq} queries x {nk} keys, numpy BLAS fp32"}
+    return out
 
 
 ST_TENSORS, ST_C = 24, 512
@@ -450,6 +511,7 @@ def main() -> int:
         sec = secondary(pkg, dev, args.steps, args.warmup, coords)
         sec += subdivide_records(pkg, dev, args.steps, args.warmup)
         sec.append(convnext_record(pkg, dev, args.steps, args.warmup))
+        sec.append(attention_record(pkg, dev, args.steps))
         sec.append(safetensors_record(pkg, args.steps))
     cpu = None
     if not args.no_cpu_baseline:

@@ -33,9 +33,11 @@ typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 
-constexpr int kThreads = 256;  // 4 waves
-constexpr int kBQ = 128;       // queries per block, 32 per wave
-constexpr float kLazy = 8.f;   // log2 headroom before the running max is raised
+constexpr int kThreads = 256;   // f32 kernel: 4 waves
+constexpr int kBQ = 128;        // f32 kernel: queries per block, 32 per wave
+constexpr int kMmaThreads = 512;  // bf16/f16 kernel: 8 waves (2 per SIMD)
+constexpr int kMmaBQ = 256;       // bf16/f16 kernel: queries per block, 32 per wave
+constexpr float kLazy = 8.f;    // log2 headroom before the running max is raised
 
 template <typename T>
 struct Mma;
@@ -73,19 +75,19 @@ __device__ __forceinline__ void segment(const int32_t* cu, int b, int64_t total,
 
 // ---------------------------------------------------------------------------------- bf16 / f16
 template <typename T, int D>
-__global__ void __launch_bounds__(kThreads)
+__global__ void __launch_bounds__(kMmaThreads)
     attn_mma_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
                     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_kv,
                     int64_t total_q, int64_t total_kv, int32_t H, float scale_log2,
                     T* __restrict__ out) {
   constexpr int BK = 64;
-  constexpr int DC = D / 8;                 // 16-byte chunks per row
-  constexpr int KS = D / 16;                // k-steps of S^T = K Q^T
-  constexpr int MT = D / 32;                // 32-dim tiles of O^T
-  constexpr int KL = BK * DC / kThreads;    // K chunks each thread stages per block
-  constexpr int VT = BK / 4 * DC;           // threads staging V (4 keys x 8 dims each)
-  constexpr int VU = BK / 4;                // 4-key units per V^T row
-  static_assert(KL >= 1 && VT <= kThreads && (D == 64 || D == 128), "tile shape");
+  constexpr int DC = D / 8;                  // 16-byte chunks per row
+  constexpr int KS = D / 16;                 // k-steps of S^T = K Q^T
+  constexpr int MT = D / 32;                 // 32-dim tiles of O^T
+  constexpr int KL = BK * DC / kMmaThreads;  // K chunks each thread stages per block
+  constexpr int VT = BK / 2 * DC;            // threads staging V (2 keys x 8 dims each)
+  constexpr int VU = BK / 4;                 // 4-key (8-byte) units per V^T row
+  static_assert(KL >= 1 && VT <= kMmaThreads && (D == 64 || D == 128), "tile shape");
   __shared__ __attribute__((aligned(16))) uint4 ks[2][BK * DC];
   __shared__ __attribute__((aligned(16))) uint2 vt[2][D * VU];
 
@@ -104,7 +106,7 @@ __global__ void __launch_bounds__(kThreads)
   };
   auto vslot = [](int d, int u) { return d * VU + (u ^ ((d >> 1) & 15)); };
 
-  for (int qt = blockIdx.x * kBQ; qt < q_len; qt += gridDim.x * kBQ) {
+  for (int qt = blockIdx.x * kMmaBQ; qt < q_len; qt += gridDim.x * kMmaBQ) {
     const int qi = qt + w * 32 + l32;
     T* orow = out + (int64_t)(q0 + qi) * rs + (int64_t)h * D;
     if (kv_len == 0) {  // no keys: zeros (uniform over the block)
@@ -118,19 +120,19 @@ __global__ void __launch_bounds__(kThreads)
 #pragma unroll
       for (int s = 0; s < KS; ++s) qf[s] = *(const uint4*)(qrow + 16 * s);
     }
-    uint4 kr[KL], vr[4];
+    uint4 kr[KL], vr[2];
     auto load = [&](int kb) {
 #pragma unroll
       for (int i = 0; i < KL; ++i) {
-        const int id = tid + kThreads * i, row = id / DC, c = id % DC;
+        const int id = tid + kMmaThreads * i, row = id / DC, c = id % DC;
         kr[i] = kb + row < kv_len ? *(const uint4*)(kbase + (int64_t)(kb + row) * rs + 8 * c)
                                   : make_uint4(0, 0, 0, 0);
       }
       if (tid < VT) {
-        const int dv = tid % DC, kq = tid / DC;
+        const int dv = tid % DC, kp = tid / DC;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int key = kb + 4 * kq + i;
+        for (int i = 0; i < 2; ++i) {
+          const int key = kb + 2 * kp + i;
           vr[i] = key < kv_len ? *(const uint4*)(vbase + (int64_t)key * rs + 8 * dv)
                                : make_uint4(0, 0, 0, 0);
         }
@@ -139,27 +141,23 @@ __global__ void __launch_bounds__(kThreads)
     auto store = [&](int buf) {
 #pragma unroll
       for (int i = 0; i < KL; ++i) {
-        const int id = tid + kThreads * i;
+        const int id = tid + kMmaThreads * i;
         ks[buf][kslot(id / DC, id % DC)] = kr[i];
       }
-      if (tid < VT) {
-        const int dv = tid % DC, kq = tid / DC;
+      if (tid < VT) {  // keys 2kp, 2kp+1 of dims 8dv..8dv+7 -> half (kp & 1) of unit kp / 2
+        const int dv = tid % DC, kp = tid / DC;
         const uint32_t* a = (const uint32_t*)&vr[0];
         const uint32_t* b = (const uint32_t*)&vr[1];
-        const uint32_t* c = (const uint32_t*)&vr[2];
-        const uint32_t* e = (const uint32_t*)&vr[3];
+        uint32_t* base = (uint32_t*)&vt[buf][0] + (kp & 1);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const int sh = 16 * (j & 1);
-          const uint32_t lo = ((a[j >> 1] >> sh) & 0xffffu) | (((b[j >> 1] >> sh) & 0xffffu) << 16);
-          const uint32_t hi = ((c[j >> 1] >> sh) & 0xffffu) | (((e[j >> 1] >> sh) & 0xffffu) << 16);
-          vt[buf][vslot(8 * dv + j, kq)] = make_uint2(lo, hi);
+          base[2 * vslot(8 * dv + j, kp >> 1)] =
+              ((a[j >> 1] >> sh) & 0xffffu) | (((b[j >> 1] >> sh) & 0xffffu) << 16);
         }
       }
     };
 
-    // m_use: the max the exponentials are taken against.  It is raised only when a block's max
-    // exceeds it by more than kLazy (log2 units), so most blocks skip the O rescale; p <= 2^kLazy.
     float m_use = -INFINITY, l_run = 0.f;
     f32x16_t o[MT];
 #pragma unroll
@@ -380,7 +378,7 @@ template <typename T, int D>
 void launch_mma(tsc_ctx* ctx, dim3 grid, const void* q, const void* k, const void* v,
                 const int32_t* cu_q, const int32_t* cu_kv, int64_t tq, int64_t tkv, int32_t H,
                 float sl2, void* out) {
-  attn_mma_kernel<T, D><<<grid, kThreads, 0, ctx->stream>>>(
+  attn_mma_kernel<T, D><<<grid, kMmaThreads, 0, ctx->stream>>>(
       (const T*)q, (const T*)k, (const T*)v, cu_q, cu_kv, tq, tkv, H, sl2, (T*)out);
 }
 
@@ -392,8 +390,9 @@ int attention_launch(tsc_ctx* ctx, int32_t dtype, const void* q, const void* k, 
                      void* out) {
   if (B == 0 || total_q == 0 || max_seqlen_q == 0) return TSC_OK;
   const float sl2 = scale * 1.4426950408889634f;  // scale * log2(e): softmax in base 2
-  // q tiles beyond the grid's x extent are covered by the kernel's tile loop
-  const unsigned gx = (unsigned)std::min<int64_t>((max_seqlen_q + kBQ - 1) / kBQ, 65535);
+  // q tiles beyond the grid's x extent are covered by the kernels' tile loops
+  const int bq = dtype == TSC_F32 ? kBQ : kMmaBQ;
+  const unsigned gx = (unsigned)std::min<int64_t>((max_seqlen_q + bq - 1) / bq, 65535);
   const dim3 grid(gx, (unsigned)H, (unsigned)B);
   ProfScope p(ctx, "attention");
   if (dtype == TSC_BF16) {
