@@ -73,6 +73,21 @@ __device__ __forceinline__ void segment(const int32_t* cu, int b, int64_t total,
   *len = (int)(e - s);
 }
 
+// Block -> (q tile, head, sequence) so that each XCD (blocks are dealt to the 8 XCDs round robin)
+// gets a contiguous run of q tiles: the blocks that stream one head's K and V share an L2.
+// XCD r holds total/8 blocks, one more for r < total % 8; block lin = 8i + r is its i-th, so the
+// map is a bijection of [0, total).
+__device__ __forceinline__ void xcd_block(int* bx, int* bh, int* bb) {
+  const int gx = gridDim.x, gy = gridDim.y;
+  const int total = gx * gy * gridDim.z;
+  const int lin = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+  const int r = lin % 8, base = total / 8, extra = total % 8;
+  const int v = r * base + min(r, extra) + lin / 8;
+  *bx = v % gx;
+  *bh = (v / gx) % gy;
+  *bb = v / (gx * gy);
+}
+
 // ---------------------------------------------------------------------------------- bf16 / f16
 template <typename T, int D>
 __global__ void __launch_bounds__(kMmaThreads)
@@ -91,10 +106,11 @@ __global__ void __launch_bounds__(kMmaThreads)
   __shared__ __attribute__((aligned(16))) uint4 ks[2][BK * DC];
   __shared__ __attribute__((aligned(16))) uint2 vt[2][D * VU];
 
+  int bx, h, bb;
+  xcd_block(&bx, &h, &bb);
   int q0, q_len, kv0, kv_len;
-  segment(cu_q, blockIdx.z, total_q, &q0, &q_len);
-  segment(cu_kv, blockIdx.z, total_kv, &kv0, &kv_len);
-  const int h = blockIdx.y;
+  segment(cu_q, bb, total_q, &q0, &q_len);
+  segment(cu_kv, bb, total_kv, &kv0, &kv_len);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, l32 = lane & 31, hf = lane >> 5;
   const int64_t rs = (int64_t)H * D;
   const T* kbase = k + (int64_t)kv0 * rs + (int64_t)h * D;
@@ -106,7 +122,7 @@ __global__ void __launch_bounds__(kMmaThreads)
   };
   auto vslot = [](int d, int u) { return d * VU + (u ^ ((d >> 1) & 15)); };
 
-  for (int qt = blockIdx.x * kMmaBQ; qt < q_len; qt += gridDim.x * kMmaBQ) {
+  for (int qt = bx * kMmaBQ; qt < q_len; qt += gridDim.x * kMmaBQ) {
     const int qi = qt + w * 32 + l32;
     T* orow = out + (int64_t)(q0 + qi) * rs + (int64_t)h * D;
     if (kv_len == 0) {  // no keys: zeros (uniform over the block)
@@ -255,16 +271,17 @@ __global__ void __launch_bounds__(kThreads)
   __shared__ __attribute__((aligned(16))) float ks[2][BK * KST];
   __shared__ __attribute__((aligned(16))) float vs[2][BK * VST];
 
+  int bx, h, bb;
+  xcd_block(&bx, &h, &bb);
   int q0, q_len, kv0, kv_len;
-  segment(cu_q, blockIdx.z, total_q, &q0, &q_len);
-  segment(cu_kv, blockIdx.z, total_kv, &kv0, &kv_len);
-  const int h = blockIdx.y;
+  segment(cu_q, bb, total_q, &q0, &q_len);
+  segment(cu_kv, bb, total_kv, &kv0, &kv_len);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, l32 = lane & 31, hf = lane >> 5;
   const int64_t rs = (int64_t)H * D;
   const float* kbase = k + (int64_t)kv0 * rs + (int64_t)h * D;
   const float* vbase = v + (int64_t)kv0 * rs + (int64_t)h * D;
 
-  for (int qt = blockIdx.x * kBQ; qt < q_len; qt += gridDim.x * kBQ) {
+  for (int qt = bx * kBQ; qt < q_len; qt += gridDim.x * kBQ) {
     const int qi = qt + w * 32 + l32;
     float* orow = out + (int64_t)(q0 + qi) * rs + (int64_t)h * D;
     if (kv_len == 0) {
@@ -392,7 +409,11 @@ int attention_launch(tsc_ctx* ctx, int32_t dtype, const void* q, const void* k, 
   const float sl2 = scale * 1.4426950408889634f;  // scale * log2(e): softmax in base 2
   // q tiles beyond the grid's x extent are covered by the kernels' tile loops
   const int bq = dtype == TSC_F32 ? kBQ : kMmaBQ;
-  const unsigned gx = (unsigned)std::min<int64_t>((max_seqlen_q + bq - 1) / bq, 65535);
+  const int64_t hb = (int64_t)H * B;  // the block index arithmetic is 32-bit
+  if (hb > (int64_t)(INT32_MAX / 16))
+    return fail(TSC_ERR_UNSUPPORTED, "attention: %lld (head, sequence) pairs", (long long)hb);
+  const unsigned gx = (unsigned)std::min<int64_t>(
+      std::min<int64_t>((max_seqlen_q + bq - 1) / bq, 65535), (INT32_MAX / 16) / hb);
   const dim3 grid(gx, (unsigned)H, (unsigned)B);
   ProfScope p(ctx, "attention");
   if (dtype == TSC_BF16) {
