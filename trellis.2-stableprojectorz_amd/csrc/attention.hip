@@ -50,6 +50,12 @@ struct Mma<__bf16> {
   static __device__ __forceinline__ uint32_t pack(float lo, float hi) {  // RNE, one cvt_pk
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
   }
+  // acc + the two packed values (v_dot2 with (1, 1)): the softmax denominator is summed over the
+  // same rounded P that the second product uses.
+  static __device__ __forceinline__ float add2(uint32_t packed, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, packed),
+                                          __builtin_bit_cast(bf16x2_t, 0x3f803f80u), acc, false);
+  }
 };
 template <>
 struct Mma<_Float16> {
@@ -60,9 +66,24 @@ struct Mma<_Float16> {
   static __device__ __forceinline__ uint32_t pack(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, f16x2_t));
   }
+  static __device__ __forceinline__ float add2(uint32_t packed, float acc) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, packed),
+                                  __builtin_bit_cast(f16x2_t, 0x3c003c00u), acc, false);
+  }
 };
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Max / sum of a value and the one held by lane l ^ 32 (both halves of the wave hold the same
+// query): v_permlane32_swap exchanges the wave halves in registers (no LDS round trip).
+__device__ __forceinline__ float pair_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 // Segment b's [begin, end) clamped into [0, total] (a malformed cu_seqlens cannot index outside).
 __device__ __forceinline__ void segment(const int32_t* cu, int b, int64_t total, int* begin,
@@ -115,12 +136,15 @@ __global__ void __launch_bounds__(kMmaThreads)
   const int64_t rs = (int64_t)H * D;
   const T* kbase = k + (int64_t)kv0 * rs + (int64_t)h * D;
   const T* vbase = v + (int64_t)kv0 * rs + (int64_t)h * D;
-  // K chunk (row, c) of a block lives at slot c ^ swz(row): 16 rows of one chunk column hit
-  // 16 distinct 4-bank groups.  V^T unit u of row d lives at u ^ ((d >> 1) & 15).
-  auto kslot = [](int row, int c) {
-    return row * DC + (c ^ (DC == 16 ? (row & 15) : ((row >> 1) & 7)));
-  };
-  auto vslot = [](int d, int u) { return d * VU + (u ^ ((d >> 1) & 15)); };
+  // LDS: 32 banks of 4 bytes; a b128 access is served 8 lanes at a time, b64 16, b32 32.
+  // K chunk (row, c) lives at slot c ^ (row & 15) (D = 128) or c ^ (row & 7) (D = 64): the 8
+  // lanes of one read step (rows r..r+7, one chunk column) and of one write step (one row, 8
+  // chunks) each cover all 32 banks.  V^T unit u of row d lives at u ^ (d & 15): the 16 rows a
+  // b64 read step touches get 16 distinct units, and rows d and d + 32 share the pattern, so the
+  // reads of the two dim tiles pair into one ds_read2st64.  A b32 write step writes one row per
+  // 32 lanes (all 32 banks).
+  auto kslot = [](int row, int c) { return row * DC + (c ^ (row & (DC - 1))); };
+  auto vslot = [](int d, int u) { return d * VU + (u ^ (d & 15)); };
 
   for (int qt = bx * kMmaBQ; qt < q_len; qt += gridDim.x * kMmaBQ) {
     const int qi = qt + w * 32 + l32;
@@ -144,8 +168,8 @@ __global__ void __launch_bounds__(kMmaThreads)
         kr[i] = kb + row < kv_len ? *(const uint4*)(kbase + (int64_t)(kb + row) * rs + 8 * c)
                                   : make_uint4(0, 0, 0, 0);
       }
-      if (tid < VT) {
-        const int dv = tid % DC, kp = tid / DC;
+      if (tid < VT) {  // 32 consecutive threads: the 32 key pairs of one 8-dim chunk
+        const int kp = tid % 32, dv = tid / 32;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
           const int key = kb + 2 * kp + i;
@@ -161,16 +185,14 @@ __global__ void __launch_bounds__(kMmaThreads)
         ks[buf][kslot(id / DC, id % DC)] = kr[i];
       }
       if (tid < VT) {  // keys 2kp, 2kp+1 of dims 8dv..8dv+7 -> half (kp & 1) of unit kp / 2
-        const int dv = tid % DC, kp = tid / DC;
+        const int kp = tid % 32, dv = tid / 32;
         const uint32_t* a = (const uint32_t*)&vr[0];
         const uint32_t* b = (const uint32_t*)&vr[1];
         uint32_t* base = (uint32_t*)&vt[buf][0] + (kp & 1);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int sh = 16 * (j & 1);
+        for (int j = 0; j < 8; ++j)  // (a.lo, b.lo) or (a.hi, b.hi) of dword j / 2
           base[2 * vslot(8 * dv + j, kp >> 1)] =
-              ((a[j >> 1] >> sh) & 0xffffu) | (((b[j >> 1] >> sh) & 0xffffu) << 16);
-        }
+              __builtin_amdgcn_perm(b[j >> 1], a[j >> 1], (j & 1) ? 0x07060302u : 0x05040100u);
       }
     };
 
@@ -205,7 +227,7 @@ __global__ void __launch_bounds__(kMmaThreads)
         float mx = s[0];
 #pragma unroll
         for (int j = 1; j < 16; ++j) mx = fmaxf(mx, s[j]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));  // -inf only for a fully masked half
+        mx = pair_max(mx);  // -inf only for a fully masked half
         if (__builtin_amdgcn_ballot_w64(mx * scale_log2 > m_use * scale_log2 + kLazy)) {
           const float m_new = fmaxf(m_use, mx);
           const float alpha = fast_exp2((m_use - m_new) * scale_log2);  // 0 while m_use = -inf
@@ -221,12 +243,10 @@ __global__ void __launch_bounds__(kMmaThreads)
         for (int half = 0; half < 2; ++half) {  // k-step: keys 16 half + {4hf.., 8+4hf..}
           float p[8];
 #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            p[i] = fast_exp2(fmaf(s[8 * half + i], scale_log2, -mc));
-            l_run += p[i];
-          }
+          for (int i = 0; i < 8; ++i) p[i] = fast_exp2(fmaf(s[8 * half + i], scale_log2, -mc));
           const uint4 pf = make_uint4(Mma<T>::pack(p[0], p[1]), Mma<T>::pack(p[2], p[3]),
                                       Mma<T>::pack(p[4], p[5]), Mma<T>::pack(p[6], p[7]));
+          l_run = Mma<T>::add2(pf.w, Mma<T>::add2(pf.z, Mma<T>::add2(pf.y, Mma<T>::add2(pf.x, l_run))));
           const int u = 8 * kt + 4 * half + hf;
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) {
@@ -240,7 +260,7 @@ __global__ void __launch_bounds__(kMmaThreads)
       if (more) store(buf ^ 1);
       __syncthreads();
     }
-    l_run += __shfl_xor(l_run, 32, 64);
+    l_run = pair_sum(l_run);
     const float inv = 1.f / l_run;
     if (qi < q_len) {
 #pragma unroll
@@ -353,7 +373,7 @@ __global__ void __launch_bounds__(kThreads)
       float mx = m_run;
 #pragma unroll
       for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[j]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      mx = pair_max(mx);
       const float mc = mx * scale_log2;
       const float alpha = fast_exp2(m_run * scale_log2 - mc);
       m_run = mx;
@@ -377,7 +397,7 @@ __global__ void __launch_bounds__(kThreads)
       if (more) store(buf ^ 1);
       __syncthreads();
     }
-    l_run += __shfl_xor(l_run, 32, 64);
+    l_run = pair_sum(l_run);
     const float inv = 1.f / l_run;
     if (qi < q_len) {
 #pragma unroll
