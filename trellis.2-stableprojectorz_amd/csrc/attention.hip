@@ -6,19 +6,21 @@
 //   n in [cu_q[b], cu_q[b+1]),  m in [cu_kv[b], cu_kv[b+1]),  rows (total, H, D) row-major.
 //   A sample with no keys gives zeros (attention.ts:57).
 //
-// One block = 4 waves = 128 queries of one (sample, head); each wave owns 32 queries and walks
-// the sample's keys in blocks of BK, with an online softmax (running max and sum per query).
+// A bf16/f16 block = 8 waves = 256 queries of one (sequence, head) (an f32 block: 4 waves, 128);
+// each wave owns 32 queries and walks the sequence's keys in blocks, with an online softmax
+// (running max and sum per query).
 // The scores are computed transposed, S^T = K Q^T (M = keys, N = queries), so that in the MFMA
 // result layout each lane holds 16 keys of ONE query (lane l: query l % 32): the row max / sum
-// need one cross-half exchange (lane l ^ 32) per block, and the output O^T = V^T P^T keeps the
+// need one cross-half exchange (lane l ^ 32) per step, and the output O^T = V^T P^T keeps the
 // same "one query per lane" layout, so the rescale by exp(m_old - m_new) is lane-local.  P^T is
 // used as the MFMA B operand straight from the score registers; the keys of each MFMA k-step are
 // therefore the score layout's rows 8(j/4) + 4(l/32) + j%4, and V is staged transposed in LDS
 // (V^T[d][key], 4-key units XOR-swizzled) so that each lane reads its two 4-key runs as 8 bytes.
 //   bf16/f16: v_mfma_f32_32x32x16 (Q^T fragment kept in registers, K block in LDS row-major with
-//             16-byte chunks XOR-swizzled by row), BK = 64, K/V double-buffered through registers.
+//             16-byte chunks XOR-swizzled by row), 64-key blocks, K/V double-buffered in LDS
+//             and prefetched one block ahead through registers.
 //   f32:      v_mfma_f32_32x32x2f32 (k-step = 2 dims / 2 keys; K and V row-major in LDS with
-//             padded strides, no transpose needed), BK = 32.
+//             padded strides, no transpose needed), 32-key blocks.
 // Bound: MFMA (4 * D flops per query-key pair) and the softmax's exp per pair.
 
 #include "tsc_internal.h"
