@@ -113,7 +113,9 @@ def load_traffic(kernel: str):
 
 def profile_pass(pkg, dev) -> None:
     """Short fixed workload for rocprofv3 --pmc runs: a 256 MiB device copy (counter scale),
-    three map builds on map512, and one conv of each conv workload."""
+    three map builds on map512, one conv of each conv workload, two subdivisions and one bf16
+    attention call."""
+    import numpy as np
     import torch
 
     wl = pkg.workloads
@@ -147,6 +149,13 @@ def profile_pass(pkg, dev) -> None:
         pkg.sparse_subdivide(sc, sf)
     torch.cuda.synchronize()
     log("subdivide done")
+    ac = wl.make_coords("resblock64_bf16")
+    cu = torch.tensor([0, *np.cumsum(np.bincount(ac[:, 0])).tolist()], dtype=torch.int32, device=dev)
+    n = int(cu[-1])
+    q, k, v = (torch.randn((n, ATTN_HEADS, ATTN_DIM), device=dev).to(torch.bfloat16) for _ in range(3))
+    pkg.sparse_attention(q, k, v, cu)
+    torch.cuda.synchronize()
+    log("attention done")
 
 
 # Decoder upsample measured on the 2-voxel shell in 128^3 (4 x ~60k voxels) with 512 bf16
