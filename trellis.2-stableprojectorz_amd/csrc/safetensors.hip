@@ -395,14 +395,6 @@ class ReadPool {
     done_.wait(g, [this] { return pending_ == 0; });
     return ok && ok_;
   }
-  ~ReadPool() {
-    {
-      std::lock_guard<std::mutex> g(m_);
-      stop_ = true;
-    }
-    cv_.notify_all();
-    for (auto& t : threads_) t.join();
-  }
 
  private:
   static bool read_range(int fd, int64_t off, char* dst, size_t b, size_t e) {
@@ -422,8 +414,7 @@ class ReadPool {
       char* dst;
       {
         std::unique_lock<std::mutex> g(m_);
-        cv_.wait(g, [&] { return stop_ || generation_ != seen; });
-        if (stop_) return;
+        cv_.wait(g, [&] { return generation_ != seen; });
         seen = generation_;
         fd = fd_, off = off_, len = len_, slice = slice_, dst = dst_;
       }
@@ -441,16 +432,26 @@ class ReadPool {
   std::vector<std::thread> threads_;
   uint64_t generation_ = 0;
   int pending_ = 0;
-  bool ok_ = true, stop_ = false;
+  bool ok_ = true;
   int fd_ = -1;
   int64_t off_ = 0;
   size_t len_ = 0, slice_ = 0;
   char* dst_ = nullptr;
 };
 
+// The pool of this process.  A forked child (a data-loader worker, say) gets a pool of its own:
+// the parent's reader threads do not exist there.  Pools are never destroyed; their idle threads
+// end with the process.
 ReadPool& read_pool() {
-  static ReadPool pool;
-  return pool;
+  static std::mutex m;
+  static ReadPool* pool = nullptr;
+  static pid_t owner = 0;
+  std::lock_guard<std::mutex> g(m);
+  if (!pool || owner != getpid()) {
+    pool = new ReadPool();
+    owner = getpid();
+  }
+  return *pool;
 }
 
 int staging(tsc_ctx* ctx) {
