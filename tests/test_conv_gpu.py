@@ -130,8 +130,9 @@ def test_conv_order_invariance_bit_exact(pkg, dev, dtype):
 
 @pytest.mark.parametrize("workload", ["map512", "wide128_bf16", "conv64_f32"])
 def test_map_conv_order(pkg, dev, workload):
-    """The conv order: inside each window of 65536 consecutive key-sorted rows, rows sorted by their
-    26-bit mask of present neighbors (tap 0 in the top bit, tap 13 left out), ties in key order."""
+    """The conv order: inside each window of 262144 consecutive key-sorted rows, rows sorted by their
+    26-bit mask of present neighbors (corner taps in the top bits, then edges, then faces, each
+    class in tap order; tap 13 left out), ties in key order."""
     coords = pkg.workloads.make_coords(workload)
     batch = int(coords[:, 0].max()) + 1
     m = _map(pkg, dev, coords, batch, pkg.workloads.grid_shape(workload))
@@ -140,11 +141,15 @@ def test_map_conv_order(pkg, dev, workload):
     perm = m.perm.cpu().numpy()
     n = len(coords)
     present = m.nbr.cpu().numpy() >= 0
+    # taps by the number of offset coordinates that are not 0 (3 = corner, 2 = edge, 1 = face)
+    cls = [sum(c != 1 for c in (v // 9, v // 3 % 3, v % 3)) for v in range(27)]
+    taps = sorted((v for v in range(27) if v != 13), key=lambda v: (-cls[v], v))
+    assert taps[:8] == [0, 2, 6, 8, 18, 20, 24, 26] and len(taps) == 26
     m26 = np.zeros(n, np.int64)
-    for v in (v for v in range(27) if v != 13):
+    for v in taps:
         m26 = (m26 << 1) | present[:, v]
     want = np.empty(n, np.int64)
-    win = 65536
+    win = 262144
     for w0 in range(0, n, win):
         rows = perm[w0:w0 + win]
         want[w0:w0 + win] = rows[np.argsort(m26[rows], kind="stable")]
