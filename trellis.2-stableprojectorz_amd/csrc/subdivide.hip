@@ -22,6 +22,16 @@ namespace {
 
 constexpr int kSubThreads = 256;  // parents per tile, threads per block
 
+// Non-temporal store of a feature piece: child rows are written once and not read back here.
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+template <typename P>
+__device__ __forceinline__ void store_nt(const P& v, P* dst) {
+  if constexpr (sizeof(P) == 16)
+    __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, v), (u32x4_t*)dst);
+  else
+    __builtin_nontemporal_store(v, dst);
+}
+
 __device__ __forceinline__ int block_excl_scan256(int v, int* wsum, int* total) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   int incl = v;
@@ -128,7 +138,7 @@ __global__ void __launch_bounds__(kSubThreads)
 #pragma unroll
     for (int ch = 0; ch < 8; ++ch) {
       if ((m >> ch) & 1u) {
-        feats_out[(f + r) * pieces + k] = v;
+        store_nt(v, &feats_out[(f + r) * pieces + k]);
         ++r;
       }
     }
