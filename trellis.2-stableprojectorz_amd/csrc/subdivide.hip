@@ -12,7 +12,7 @@
 // tile an exclusive block scan of the per-parent counts gives each parent's first child row.
 // Features are copied in 16-byte pieces (4- or 2-byte when the row size requires): consecutive
 // threads take consecutive pieces of one parent row, load each piece once and store it to every
-// kept child, so loads and stores are coalesced runs of whole rows.  Bound: HBM, bytes per parent
+// kept child (non-temporal stores), so loads and stores are coalesced runs of whole rows.  Bound: HBM, bytes per parent
 // = 16 + R (coords and row in) + k * (16 + R) (k kept children out), R = C * element size.
 
 #include "tsc_internal.h"
