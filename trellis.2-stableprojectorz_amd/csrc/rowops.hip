@@ -55,6 +55,8 @@ __device__ __forceinline__ float wave_sum(float v) {
 __device__ __forceinline__ float silu_f(float x) { return x * (1.0f / (1.0f + __expf(-x))); }
 
 // MAXV = max 16-byte vectors per lane (row length <= 64 * MAXV * Vec<T>::n).
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+
 template <typename T, int MAXV>
 __global__ void __launch_bounds__(256)
     layernorm_kernel(const T* x, int64_t N, int32_t C, const T* __restrict__ gamma,
@@ -111,7 +113,8 @@ __global__ void __launch_bounds__(256)
         float t = (v[k][e] - mean) * inv * g[e] + b[e];
         o[e] = apply_silu ? silu_f(t) : t;
       }
-      yr[vi] = pack<T>(o);
+      // non-temporal: the normalised rows are read back only by the next layer's kernel
+      __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, pack<T>(o)), (u32x4_t*)&yr[vi]);
     }
   }
 }
