@@ -10,12 +10,23 @@
 
 #include <hipblaslt/hipblaslt.h>
 
+#include <map>
+#include <tuple>
+
 #include "tsc_internal.h"
 
 namespace tsc {
 namespace {
 
 constexpr size_t kBlasWorkspace = (size_t)64 << 20;
+constexpr int kTuneCandidates = 16;          // heuristic results timed per new shape
+constexpr size_t kTuneScratch = (size_t)512 << 20;  // largest tuning output (fewer rows above)
+
+// Fastest algorithm per (dtype, rows timed, Cin, Cout, bias, residual), chosen once per context
+// by timing the heuristic's candidates (the library's first pick is up to ~20 % slower on some
+// of the ConvNeXt shapes).
+using AlgoKey = std::tuple<int32_t, int64_t, int32_t, int32_t, bool, bool>;
+using AlgoCache = std::map<AlgoKey, hipblasLtMatmulAlgo_t>;
 
 hipDataType blas_type(int32_t dtype) {
   switch (dtype) {
@@ -49,6 +60,8 @@ struct BlasCall {
 void blas_destroy(tsc_ctx* ctx) {
   if (ctx->blaslt) hipblasLtDestroy((hipblasLtHandle_t)ctx->blaslt);
   ctx->blaslt = nullptr;
+  delete (AlgoCache*)ctx->blas_algos;
+  ctx->blas_algos = nullptr;
 }
 
 int linear_launch(tsc_ctx* ctx, int32_t dtype, const void* x, int64_t N, int32_t Cin,
@@ -102,18 +115,87 @@ int linear_launch(tsc_ctx* ctx, int32_t dtype, const void* x, int64_t N, int32_t
                       c.pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb, sizeof(wsb)),
                   "workspace preference");
   if (st) return st;
+  const float alpha = 1.f, beta = residual ? 1.f : 0.f;
+  const hipblasLtHandle_t lt = (hipblasLtHandle_t)ctx->blaslt;
+  if (!ctx->blas_algos) ctx->blas_algos = new AlgoCache();
+  AlgoCache& cache = *(AlgoCache*)ctx->blas_algos;
+  // Tuning runs write a scratch output (an in-place residual is never accumulated twice), on at
+  // most kTuneScratch bytes of rows.
+  const size_t esz = dtype == TSC_F32 ? 4 : 2;
+  const int64_t nt = std::min<int64_t>(N, std::max<int64_t>(1, (int64_t)(kTuneScratch / (esz * Cout))));
+  const AlgoKey key{dtype, nt, Cin, Cout, bias != nullptr, residual != nullptr};
+  auto it = cache.find(key);
+  if (it == cache.end()) {
+    BlasCall tc;  // layouts of the tuning problem (nt rows)
+    st = blas_check(hipblasLtMatrixLayoutCreate(&tc.lb, t, Cin, nt, Cin), "layout B (tune)");
+    if (st) return st;
+    st = blas_check(hipblasLtMatrixLayoutCreate(&tc.lc, t, Cout, nt, Cout), "layout C/D (tune)");
+    if (st) return st;
+    hipblasLtMatmulHeuristicResult_t res[kTuneCandidates];
+    int found = 0;
+    st = blas_check(hipblasLtMatmulAlgoGetHeuristic(lt, c.desc, c.la, tc.lb, tc.lc, tc.lc, c.pref,
+                                                    kTuneCandidates, res, &found),
+                    "heuristic");
+    if (st) return st;
+    if (found < 1)
+      return fail(TSC_ERR_UNSUPPORTED, "linear: no hipBLASLt algorithm for %dx%d", Cin, Cout);
+    int best = 0;
+    if (found > 1) {
+      void* scratch;
+      st = workspace(ctx, (size_t)nt * Cout * esz, &scratch);
+      if (st) return st;
+      hipEvent_t e0, e1;
+      st = check_hip(hipEventCreate(&e0), "linear tune event");
+      if (st) return st;
+      st = check_hip(hipEventCreate(&e1), "linear tune event");
+      if (st) {
+        (void)hipEventDestroy(e0);
+        return st;
+      }
+      float best_ms = 0.f;
+      bool have = false;
+      for (int i = 0; i < found; ++i) {
+        const void* cin = residual ? residual : scratch;
+        auto run = [&] {
+          return hipblasLtMatmul(lt, c.desc, &alpha, weight, c.la, x, tc.lb, &beta, cin, tc.lc,
+                                 scratch, tc.lc, &res[i].algo, ws, kBlasWorkspace, ctx->stream);
+        };
+        if (run() != HIPBLAS_STATUS_SUCCESS) continue;  // warm-up; unusable candidates drop out
+        (void)hipEventRecord(e0, ctx->stream);
+        bool ok = run() == HIPBLAS_STATUS_SUCCESS && run() == HIPBLAS_STATUS_SUCCESS;
+        (void)hipEventRecord(e1, ctx->stream);
+        float ms = 0.f;
+        ok = ok && hipEventSynchronize(e1) == hipSuccess &&
+             hipEventElapsedTime(&ms, e0, e1) == hipSuccess;
+        if (ok && (!have || ms < best_ms)) {
+          best_ms = ms;
+          best = i;
+          have = true;
+        }
+      }
+      (void)hipEventDestroy(e0);
+      (void)hipEventDestroy(e1);
+      (void)hipGetLastError();
+    }
+    it = cache.emplace(key, res[best].algo).first;
+  }
+  ProfScope p(ctx, "linear");
+  if (hipblasLtMatmul(lt, c.desc, &alpha, weight, c.la, x, c.lb, &beta, residual ? residual : out,
+                      c.lc, out, c.lc, &it->second, ws, kBlasWorkspace,
+                      ctx->stream) == HIPBLAS_STATUS_SUCCESS)
+    return TSC_OK;
+  // The algorithm was timed on fewer rows and does not take this many: the library's pick.
+  (void)hipGetLastError();
   hipblasLtMatmulHeuristicResult_t res;
   int found = 0;
-  st = blas_check(hipblasLtMatmulAlgoGetHeuristic((hipblasLtHandle_t)ctx->blaslt, c.desc, c.la,
-                                                  c.lb, c.lc, c.lc, c.pref, 1, &res, &found),
+  st = blas_check(hipblasLtMatmulAlgoGetHeuristic(lt, c.desc, c.la, c.lb, c.lc, c.lc, c.pref, 1,
+                                                  &res, &found),
                   "heuristic");
   if (st) return st;
   if (found < 1) return fail(TSC_ERR_UNSUPPORTED, "linear: no hipBLASLt algorithm for %dx%d", Cin, Cout);
-  const float alpha = 1.f, beta = residual ? 1.f : 0.f;
-  ProfScope p(ctx, "linear");
-  return blas_check(hipblasLtMatmul((hipblasLtHandle_t)ctx->blaslt, c.desc, &alpha, weight, c.la, x,
-                                    c.lb, &beta, residual ? residual : out, c.lc, out, c.lc,
-                                    &res.algo, ws, kBlasWorkspace, ctx->stream),
+  return blas_check(hipblasLtMatmul(lt, c.desc, &alpha, weight, c.la, x, c.lb, &beta,
+                                    residual ? residual : out, c.lc, out, c.lc, &res.algo, ws,
+                                    kBlasWorkspace, ctx->stream),
                     "matmul");
 }
 

@@ -35,6 +35,7 @@ struct tsc_ctx {
   void* blaslt = nullptr;
   void* ws_blas = nullptr;
   size_t ws_blas_bytes = 0;
+  void* blas_algos = nullptr;  // tuned algorithm per linear shape (linear.hip)
   // Pinned host chunks (and their last copies' events) of the safetensors reader.
   void* st_pin[2] = {nullptr, nullptr};
   hipEvent_t st_ev[2] = {nullptr, nullptr};
