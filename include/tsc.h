@@ -158,7 +158,10 @@ int tsc_resblock(tsc_ctx* ctx, int32_t dtype, const void* x, const int32_t* nbr,
 /* ---- per-voxel linear layer ---------------------------------------------------------------- */
 /* out (N,Cout) = x (N,Cin) * weight^T + bias (+ residual); weight (Cout,Cin) as nn.Linear, bias
  * (Cout) or NULL, residual (N,Cout) or NULL (it may alias out; x may not).  All `dtype`, fp32
- * accumulation, one hipBLASLt GEMM (bias epilogue, residual as its C operand).
+ * accumulation, one hipBLASLt GEMM (bias epilogue, residual as its C operand).  The first call
+ * of a shape on a context times the library's candidate algorithms (into scratch rows, so an
+ * in-place residual is not applied twice) and synchronizes the stream once; later calls only
+ * enqueue.
  * Replaces sparseLinear (src/sparse/ops/linear.ts:9-29) and the matmul + add pairs of the sparse
  * ConvNeXt block (src/models/sparse_unet_vae_decoder.ts:48-78). */
 int tsc_linear(tsc_ctx* ctx, int32_t dtype, const void* x, int64_t N, int32_t Cin,
