@@ -188,7 +188,9 @@ int tsc_subdivide(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t dtype,
 /* Scaled-dot-product attention over packed variable-length sequences:
  *   out[n,h,:] = softmax_m(q[n,h,:] . k[m,h,:] * scale) v[m,h,:]
  * for n in [cu_seqlens_q[b], cu_seqlens_q[b+1]) and m in [cu_seqlens_kv[b], cu_seqlens_kv[b+1]),
- * b < B.  A sequence with no keys gives zeros.
+ * b < B.  A sequence with no keys gives zeros; rows of out outside [cu_seqlens_q[0],
+ * cu_seqlens_q[B]) are not written (the Python host zero-fills them, as the reference's zero-
+ * initialised output does, attention.ts:49).
  *   q, out (total_q, num_heads, head_dim), k, v (total_kv, num_heads, head_dim): `dtype`,
  *     row-major, 16-byte aligned; out must not alias an input.  head_dim 64 or 128.
  *   cu_seqlens_q / cu_seqlens_kv  device int32 (B+1), non-decreasing, within [0, total]

@@ -125,6 +125,19 @@ def test_slat_sized_bf16_sampled_rows(pkg, dev):
     _check(out, q, k, v, cu, cu, torch.bfloat16, rows=rows)
 
 
+def test_rows_outside_every_sequence_are_zero(pkg, dev):
+    """cu_seqlens need not cover every row: rows before cu[0] and after cu[B] come out zero, as the
+    reference's zero-initialised output (attention.ts:49) leaves them."""
+    rng = np.random.default_rng(8)
+    cu = [5, 40, 90]
+    q, k, v = _inputs(rng, 100, 100, 2, 64, torch.bfloat16)
+    print("  attention partial coverage", flush=True)
+    out = pkg.sparse_attention(q.to(dev), k.to(dev), v.to(dev), cu, cu)
+    torch.cuda.synchronize()
+    assert not out[:5].any() and not out[90:].any()
+    _check(out, q, k, v, cu, cu, torch.bfloat16)
+
+
 def test_attention_rejects_bad_arguments(pkg, dev):
     x = torch.zeros(10, 2, 64, device=dev, dtype=torch.bfloat16)
     with pytest.raises(pkg.TscError):

@@ -323,7 +323,10 @@ def sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqle
         raise TscError(_lib.TSC_ERR_INVALID, "cu_seqlens_q and cu_seqlens_kv differ in length")
     b = len(cq_host) - 1
     if out is None:
-        out = torch.empty((tq, h, d), dtype=q.dtype, device=q.device)
+        # rows outside every sequence stay zero, as in the reference's zero-initialised output
+        # (attention.ts:49); the kernel writes every row inside one
+        covered = b > 0 and cq_host[0] == 0 and cq_host[-1] == tq
+        out = (torch.empty if covered else torch.zeros)((tq, h, d), dtype=q.dtype, device=q.device)
     elif out.numel() != tq * h * d or out.dtype != q.dtype:
         raise TscError(_lib.TSC_ERR_INVALID, "out has the wrong size or dtype")
     max_q = int((cq_host[1:] - cq_host[:-1]).max()) if b > 0 else 0
