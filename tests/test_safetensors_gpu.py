@@ -101,6 +101,11 @@ def test_raw_types_and_errors(pkg, dev, tmp_path):
             np.testing.assert_array_equal(got.cpu().numpy(), arr)
             np.testing.assert_array_equal(sf.read_tensor_raw(name).cpu().numpy(), S.read_raw(p, name))
         assert sf.read_tensor("empty", torch.float32).shape == (0, 7)
+        # readTensorF32 of a non-float tensor: its bytes as float32 values (weights.ts:178-186)
+        np.testing.assert_array_equal(sf.read_tensor_f32("i64").cpu().numpy(),
+                                      d["i64"].view(np.float32))
+        with pytest.raises(pkg.TscError):
+            sf.read_tensor_f32("u8")  # 33 bytes: not a whole number of float32 values
         with pytest.raises(pkg.TscError) as ei:
             sf.read_tensor("i32", torch.float32)
         assert ei.value.status == 2

@@ -192,8 +192,17 @@ class SafetensorsFile:
         return self._load(name, _OUT_CODES[dtype], out)
 
     def read_tensor_f32(self, name: str, device=None) -> torch.Tensor:
-        """readTensorF32 (weights.ts:150-177): float tensors widened to float32 on the device."""
-        return self.read_tensor(name, torch.float32, device)
+        """readTensorF32 (weights.ts:150-188): F32/F16/BF16 tensors widened to float32 on the
+        device (shaped); any other dtype's stored bytes reinterpreted as a flat float32 array, as
+        the reference's `new Float32Array(raw)` does (its byte length must be a multiple of 4)."""
+        e = self._entry(name)
+        if e.dtype in ("F32", "F16", "BF16"):
+            return self.read_tensor(name, torch.float32, device)
+        raw = self.read_tensor_raw(name, device)
+        if raw.numel() % 4:
+            raise TscError(_lib.TSC_ERR_INVALID,
+                           f"{name}: {raw.numel()} bytes are not a whole number of float32 values")
+        return raw.view(torch.float32)
 
     def get_tensor(self, name: str, device=None) -> torch.Tensor:
         """The model loader's getTensor (loader.ts:154-160): read_tensor_f32 with its shape."""
