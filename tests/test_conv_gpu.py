@@ -76,6 +76,33 @@ def test_conv_fp16_narrow_full_size(pkg, dev, ci, co):
     assert err <= TOL[torch.float16], err
 
 
+@pytest.mark.parametrize("ci,co", [(32, 32), (32, 64)])
+def test_conv_fp32_narrow_full_size(pkg, dev, ci, co):
+    """fp32 32->32 runs the wave-tile kernel on v_mfma_f32_16x16x4f32; 32->64 the tile path."""
+    err, *_ = _workload_conv(pkg, dev, "narrow512_f16", ci, co, torch.float32, sample_rows=20000)
+    assert err <= TOL[torch.float32], err
+
+
+def test_conv_fp32_narrow_residual_in_place(pkg, dev):
+    """fp32 narrow kernel epilogue: bias + residual, out aliasing the residual (16-byte stores)."""
+    coords = pkg.workloads.make_coords("conv64_f32")
+    n = len(coords)
+    m = _map(pkg, dev, coords, int(coords[:, 0].max()) + 1, pkg.workloads.grid_shape("conv64_f32"))
+    nbr = m.nbr.cpu().numpy()
+    dt = torch.float32
+    f, f64 = _rounded(pkg.workloads.features(n, 32, 4), dt, dev)
+    w, w64 = _rounded(pkg.workloads.conv_weight(32, 32, 5), dt, dev)
+    b, b64 = _rounded(np.linspace(-1, 1, 32).astype(np.float32), dt, dev)
+    r, r64 = _rounded(pkg.workloads.features(n, 32, 6), dt, dev)
+    print(f"  conv fp32 narrow residual N={n}", flush=True)
+    base = oracle.conv(f64, w64, b64, nbr)
+    r2 = r.clone()
+    pkg.sparse_conv3d(f, w, b, m, epilogue="residual", residual=r2, out=r2)
+    assert rel_err(r2.cpu().numpy(), base + r64) <= 1e-4
+    out = pkg.sparse_conv3d(f, w, None, m)
+    assert rel_err(out.cpu().numpy(), oracle.conv(f64, w64, None, nbr)) <= 1e-4
+
+
 def test_conv_bf16_wide_full_size(pkg, dev):
     err, *_ = _workload_conv(pkg, dev, "wide128_bf16", 512, 512, torch.bfloat16, sample_rows=600)
     assert err <= TOL[torch.bfloat16], err

@@ -781,6 +781,17 @@ __device__ __forceinline__ void mfma16_piece<_Float16>(const uint4& a, const uin
                                                __builtin_bit_cast(f16x8_t, b), acc, 0, 0, 0);
 }
 
+// Eight v_mfma_f32_16x16x4f32 steps over the 8 fp32 values (two 16-byte pieces) of each operand.
+__device__ __forceinline__ void mfma16_f32x8(const uint4 (&a)[2], const uint4 (&b)[2],
+                                             f32x4_t& acc) {
+  const uint32_t* av = (const uint32_t*)a;
+  const uint32_t* bv = (const uint32_t*)b;
+#pragma unroll
+  for (int s = 0; s < 8; ++s)
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(av[s]), __uint_as_float(bv[s]),
+                                               acc, 0, 0, 0);
+}
+
 template <typename T, int CO, int EPI, int NT>
 __global__ void __launch_bounds__(NT)
     conv_narrow_kernel(const T* __restrict__ feats, const T* __restrict__ weight,
@@ -788,7 +799,8 @@ __global__ void __launch_bounds__(NT)
                        const int32_t* __restrict__ order, int64_t N, int32_t n_tiles,
                        int32_t tiles_per_xcd, const T* residual, T* out) {
   constexpr int CI = 32;
-  constexpr int PPR = 4;            // 16-byte pieces per weight / feature row
+  constexpr int PL = sizeof(T) == 4 ? 2 : 1;  // 16-byte pieces per lane per row (fp32: 32 bytes)
+  constexpr int PPR = 4 * PL;                 // 16-byte pieces per weight / feature row
   constexpr int CB = CO / 16;       // 16-column output blocks
   constexpr int NW = NT / 64;
   constexpr int R = kNarrowSlots;
@@ -799,10 +811,16 @@ __global__ void __launch_bounds__(NT)
   const int l16 = lane & 15, q = lane >> 4;
 
   // Stage W (Co,27,Ci): global piece g = (co*27 + v)*PPR + p  ->  LDS [(v*CO + co)*PPR + swz(p)].
+  // fp32 rows are 128 bytes: piece p of row co sits at p ^ (co & 7), so the 8 lanes of one
+  // 16-byte read step (8 consecutive co, one piece) cover all 32 banks.
+  auto wslot = [](int co, int p) {
+    if constexpr (sizeof(T) == 4) return p ^ (co & 7);
+    else return swz<PPR>(co, p);
+  };
   const uint4* wq = (const uint4*)weight;
   for (int g = tid; g < CO * kTaps * PPR; g += NT) {
     const int p = g % PPR, cv = g / PPR, v = cv % kTaps, co = cv / kTaps;
-    sW[(v * CO + co) * PPR + swz<PPR>(co, p)] = wq[g];
+    sW[(v * CO + co) * PPR + wslot(co, p)] = wq[g];
   }
   __syncthreads();
   int32_t* const nbw = sNb[wid];
@@ -882,10 +900,10 @@ __global__ void __launch_bounds__(NT)
     // Slot ring: slot r holds tap vt[r] (-1 past the last tap: zero-block pieces, never used).
     uint32_t rem = tmask;
     int vt[R];
-    uint4 fr[R][2];
-    // Loads are coalesced (lanes 4j..4j+3 read the four pieces of row 16*rb + j, one 64-byte
-    // request per row); the fragment the MFMA wants in lane t (row t%16, piece t/16) is then
-    // fetched from lane 4*(t%16) + t/16 with ds_bpermute right before use.
+    uint4 fr[R][2][PL];
+    // Loads are coalesced (lanes 4j..4j+3 read the four quarters of row 16*rb + j, one request
+    // per row); the fragment the MFMA wants in lane t (row t%16, quarter t/16) is then fetched
+    // from lane 4*(t%16) + t/16 with ds_bpermute right before use.
     auto fill = [&](int r) {
       const int v = rem ? __builtin_ctz(rem) : -1;
       rem &= rem - 1u;
@@ -895,7 +913,8 @@ __global__ void __launch_bounds__(NT)
         const int32_t sidx = v >= 0 ? nbw[(rb * 16 + (lane >> 2)) * kTaps + v] : -1;
         const T* src = sidx >= 0 ? feats + (int64_t)sidx * CI + (lane & 3) * 8
                                  : (const T*)g_zero + (lane & 3) * 8;
-        fr[r][rb] = *(const uint4*)src;
+#pragma unroll
+        for (int h = 0; h < PL; ++h) fr[r][rb][h] = *(const uint4*)(src + h * (16 / sizeof(T)));
       }
     };
     const int src_lane = 4 * l16 + q;
@@ -914,13 +933,26 @@ __global__ void __launch_bounds__(NT)
       for (int r = 0; r < R; ++r) {
         if (t0 + r < ntaps) {
           const int v = vt[r];
-          const uint4 b0 = to_mfma(fr[r][0]), b1 = to_mfma(fr[r][1]);
+          uint4 b0[PL], b1[PL];
+#pragma unroll
+          for (int h = 0; h < PL; ++h) {
+            b0[h] = to_mfma(fr[r][0][h]);
+            b1[h] = to_mfma(fr[r][1][h]);
+          }
 #pragma unroll
           for (int cb = 0; cb < CB; ++cb) {
             const int co = cb * 16 + l16;
-            const uint4 wa = sW[(v * CO + co) * PPR + swz<PPR>(co, q)];
-            mfma16_piece<T>(wa, b0, acc[0][cb]);
-            mfma16_piece<T>(wa, b1, acc[1][cb]);
+            if constexpr (sizeof(T) == 4) {
+              // k-step s of v_mfma_f32_16x16x4f32: lane (co / row, quarter q) holds ci 8q + s
+              const uint4 wa[2] = {sW[(v * CO + co) * PPR + wslot(co, 2 * q)],
+                                   sW[(v * CO + co) * PPR + wslot(co, 2 * q + 1)]};
+              mfma16_f32x8(wa, b0, acc[0][cb]);
+              mfma16_f32x8(wa, b1, acc[1][cb]);
+            } else {
+              const uint4 wa = sW[(v * CO + co) * PPR + wslot(co, q)];
+              mfma16_piece<T>(wa, b0[0], acc[0][cb]);
+              mfma16_piece<T>(wa, b1[0], acc[1][cb]);
+            }
           }
         }
         fill(r);
@@ -938,22 +970,23 @@ __global__ void __launch_bounds__(NT)
         float x[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) x[i] = acc[rb][cb][i];
+        struct alignas(4 * sizeof(T)) V4 {
+          T v[4];
+        };
         if (bias) {
-          const uint2 bb = *(const uint2*)(bias + c0);
-          const T* bt = (const T*)&bb;
+          const V4 bt = *(const V4*)(bias + c0);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) x[i] += to_f32<T>(bt[i]);
+          for (int i = 0; i < 4; ++i) x[i] += to_f32<T>(bt.v[i]);
         }
         if (EPI == TSC_EPI_BIAS_RESIDUAL) {
-          const uint2 rr = *(const uint2*)(residual + (int64_t)row * CO + c0);
-          const T* rt = (const T*)&rr;
+          const V4 rt = *(const V4*)(residual + (int64_t)row * CO + c0);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) x[i] += to_f32<T>(rt[i]);
+          for (int i = 0; i < 4; ++i) x[i] += to_f32<T>(rt.v[i]);
         }
-        T y[4];
+        V4 y;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) y[i] = from_f32<T>(x[i]);
-        *(uint2*)(out + (int64_t)row * CO + c0) = *(const uint2*)y;
+        for (int i = 0; i < 4; ++i) y.v[i] = from_f32<T>(x[i]);
+        *(V4*)(out + (int64_t)row * CO + c0) = y;
       }
     }
     my_row = row_next;
@@ -966,7 +999,7 @@ int launch_narrow(tsc_ctx* ctx, const ConvArgs& a) {
   // Block size: 8 waves (one block per CU) when the weights + per-wave neighbor slices fit.
   // Measured on the 1.5M-voxel shell: 8 waves beat 16 (fewer concurrent gathers thrash the
   // L1/L2 less) and 4 (too little memory-level parallelism).
-  constexpr int kW = kTaps * CO * 4 * 16;
+  constexpr int kW = kTaps * CO * 4 * 16 * (sizeof(T) == 4 ? 2 : 1);
   constexpr int kPerWave = kTaps * 32 * 4;
   constexpr int NW = std::min(8, (163840 - 1024 - kW) / kPerWave);
   static_assert(NW >= 4, "narrow kernel: weights too large for LDS");
@@ -976,7 +1009,8 @@ int launch_narrow(tsc_ctx* ctx, const ConvArgs& a) {
   int32_t blocks = std::min<int32_t>(256, (n_tiles + NW - 1) / NW);
   blocks = std::max<int32_t>(8, (blocks + 7) / 8 * 8);
   static const std::string name = std::string("conv_narrow_") +
-      (std::is_same<T, __bf16>::value ? "bf16" : "f16") + "_32x" + std::to_string(CO) +
+      (std::is_same<T, __bf16>::value ? "bf16" : sizeof(T) == 4 ? "f32" : "f16") + "_32x" +
+      std::to_string(CO) +
       (EPI == TSC_EPI_BIAS_RESIDUAL ? "_res" : "");
   ProfScope p(ctx, name.c_str());
   conv_narrow_kernel<T, CO, EPI, NT><<<blocks, NT, 0, ctx->stream>>>(
@@ -999,6 +1033,10 @@ int dispatch_tiles(tsc_ctx* ctx, const ConvArgs& a) {
     // Narrow 16-bit rows: wave-level gather tiles (weights in LDS).
     if (a.Ci == 32 && a.Co == 32) return launch_narrow<T, 32, EPI>(ctx, a);
     if (a.Ci == 32 && a.Co == 64) return launch_narrow<T, 64, EPI>(ctx, a);
+  } else {
+    // fp32, Ci = Co = 32: the same wave tiles on v_mfma_f32_16x16x4f32 (the 32->64 weights do
+    // not fit in LDS beside the neighbor slices).
+    if (a.Ci == 32 && a.Co == 32) return launch_narrow<T, 32, EPI>(ctx, a);
   }
   if (a.Ci * (int)sizeof(T) <= 64) {
     // Other narrow input rows: one K chunk per tap -> register-staged double buffer.
