@@ -745,8 +745,10 @@ int launch_cfg(tsc_ctx* ctx, const ConvArgs& a) {
   return check_hip(hipGetLastError(), "conv launch");
 }
 
-// Narrow-channel kernel (16-bit types, Ci = 32: one 64-byte row per neighbor).  Every wave works
-// alone on tiles of 32 output rows; there is no block barrier after the weights are staged.  The
+// Narrow-channel kernel (Ci = 32: one 64-byte row per neighbor for 16-bit types, 128 bytes for
+// fp32).  Every wave works alone on tiles of 32 output rows; there is no block barrier after the
+// weights are staged.  fp32 keeps the same layout with two 16-byte pieces per lane and runs each
+// tap as eight v_mfma_f32_16x16x4f32 steps (lane quarter q holds channels 8q..8q+7).  The
 // design minimises distinct cache lines per memory instruction, which bounds the L1/TA rate of
 // gather-heavy code:
 //   rows      the 32 rows of the tile (entries of `order`); their 32 x 27 neighbor indices are
