@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define TSC_VERSION 4
+#define TSC_VERSION 5
 
 /* Status codes returned by every entry point. */
 enum tsc_status {
@@ -119,6 +119,20 @@ int tsc_map_build(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t B, int
 int tsc_map_conv_order(tsc_ctx* ctx, const int32_t* nbr, const int32_t* perm, int64_t N,
                        int32_t* order_out);
 
+/* Gather plan for the narrow convs (Ci = 32 in fp16/bf16): rows in 64-row tiles along a Morton
+ * (Z-order) curve of the coordinates, each tile's distinct neighbor rows listed once, and a
+ * per-(row, tap) slot table into that list.  tsc_conv_planned then gathers each distinct row
+ * once per tile instead of once per (row, tap) reference (~1.9 instead of ~9 row reads per
+ * output row on a 1-voxel shell).  coords / nbr / B,X,Y,Z as given to tsc_map_build and its
+ * output; plan: device buffer of tsc_map_gather_plan_bytes(N) bytes, 256-byte aligned (-1 from
+ * tsc_map_gather_plan_bytes means N is out of range).  Stream-ordered; it uses the context's
+ * workspace for the curve sort.
+ * No counterpart in the reference: an acceleration structure derived from the neighbor map,
+ * meant to be cached beside it (the reference caches the map per tensor, conv3d.ts:144-148). */
+int64_t tsc_map_gather_plan_bytes(int64_t N);
+int tsc_map_gather_plan(tsc_ctx* ctx, const int32_t* coords, const int32_t* nbr, int64_t N,
+                        int32_t B, int32_t X, int32_t Y, int32_t Z, void* plan);
+
 /* ---- convolution -------------------------------------------------------------------------- */
 /* out[n,co] = bias[co] + sum_{v: nbr[n,v]>=0} sum_ci feats[nbr[n,v],ci] * W[co,v,ci]
  *   feats (N,Ci), weight (Co,3,3,3,Ci), bias (Co) or NULL, out (N,Co): all `dtype`, row-major.
@@ -136,6 +150,15 @@ int tsc_conv_fused(tsc_ctx* ctx, int32_t dtype, const void* feats, const void* w
                    const void* bias, const int32_t* nbr, const int32_t* order, int64_t N,
                    int32_t Ci, int32_t Co, int32_t epilogue, const void* residual,
                    const void* ln_gamma, const void* ln_beta, float eps, void* out);
+
+/* tsc_conv_fused with a gather plan (tsc_map_gather_plan of the same coordinate set and map)
+ * in place of the row order.  Ci = 32 with Co = 32 or 64 in fp16/bf16 runs the planned
+ * kernel; other shapes run the tsc_conv_fused kernels in the plan's row order.  Same results
+ * as tsc_conv_fused, bit for bit.  Replaces conv3d.ts:154-221 for the decoder's narrow convs. */
+int tsc_conv_planned(tsc_ctx* ctx, int32_t dtype, const void* feats, const void* weight,
+                     const void* bias, const int32_t* nbr, const void* plan, int64_t N,
+                     int32_t Ci, int32_t Co, int32_t epilogue, const void* residual,
+                     const void* ln_gamma, const void* ln_beta, float eps, void* out);
 
 /* ---- row ops (the ResBlock's epilogue semantics) ------------------------------------------ */
 /* y = (x-mean)/sqrt(var+eps)*gamma+beta per row of C, fp32 math; optional SiLU after it.

@@ -11,7 +11,7 @@ def test_library_exports_every_declared_symbol(pkg):
     assert len(declared) >= 18
     missing = [s for s in declared if not hasattr(lib, s)]
     assert not missing, missing
-    assert lib.tsc_version() == 4
+    assert lib.tsc_version() == 5
 
 
 def test_null_context_and_bad_arguments_fail_cleanly(pkg):
@@ -29,6 +29,25 @@ def test_null_context_and_bad_arguments_fail_cleanly(pkg):
     st = lib.tsc_ctx_create(-1, None, ctypes.byref(out))
     assert st != 0 and lib.tsc_last_error()
     assert lib.tsc_ctx_destroy(None) == 0
+
+
+def test_gather_plan_bytes(pkg):
+    """Plan size = five 256-byte aligned arrays over T = ceil(N/64) tiles: rows (T*64 int32),
+    counts (T int32), tap masks (T*4 uint32), distinct-row lists (T*256 int32), slot tables
+    (T*1792 bytes); -1 for N out of range."""
+    lib = pkg.load_library()
+    lib.tsc_map_gather_plan_bytes.restype = ctypes.c_int64
+    lib.tsc_map_gather_plan_bytes.argtypes = [ctypes.c_int64]
+    al = lambda v: (v + 255) // 256 * 256
+    for n in (0, 1, 64, 65, 1514003):
+        t = (n + 63) // 64
+        want = al(t * 256) + al(t * 4) + al(t * 16) + al(t * 1024) + al(t * 1792)
+        assert lib.tsc_map_gather_plan_bytes(n) == want
+    assert lib.tsc_map_gather_plan_bytes(-1) == -1
+    assert lib.tsc_map_gather_plan_bytes(2 ** 31) == -1
+    P = ctypes.c_void_p
+    st = lib.tsc_map_gather_plan(None, P(16), P(16), 10, 1, 8, 8, 8, P(256))
+    assert st == 1 and b"null context" in lib.tsc_last_error()
 
 
 def test_ops_refuse_cpu_tensors(pkg):

@@ -61,6 +61,10 @@ _SIGNATURES = {
     "tsc_map_key_bytes": (_I32, [_I32, _I32, _I32, _I32]),
     "tsc_map_build": (_I32, [_P, _P, _I64, _I32, _I32, _I32, _I32, _P, _P, _I32, _P, _P, _P, _P]),
     "tsc_map_conv_order": (_I32, [_P, _P, _P, _I64, _P]),
+    "tsc_map_gather_plan_bytes": (_I64, [_I64]),
+    "tsc_map_gather_plan": (_I32, [_P, _P, _P, _I64, _I32, _I32, _I32, _I32, _P]),
+    "tsc_conv_planned": (_I32, [_P, _I32, _P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _P, _P, _P,
+                                _F32, _P]),
     "tsc_conv": (_I32, [_P, _I32, _P, _P, _P, _P, _P, _I64, _I32, _I32, _P]),
     "tsc_conv_fused": (_I32, [_P, _I32, _P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _P, _P, _P,
                               _F32, _P]),

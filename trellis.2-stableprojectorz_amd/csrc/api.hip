@@ -320,6 +320,56 @@ int tsc_map_conv_order(tsc_ctx* ctx, const int32_t* nbr, const int32_t* perm, in
   return tsc::conv_order_launch(ctx, nbr, perm, N, order_out);
 }
 
+int64_t tsc_map_gather_plan_bytes(int64_t N) {
+  if (N < 0 || N > INT32_MAX - 64) return -1;
+  return (int64_t)tsc::plan_layout(N).total;
+}
+
+int tsc_map_gather_plan(tsc_ctx* ctx, const int32_t* coords, const int32_t* nbr, int64_t N,
+                        int32_t B, int32_t X, int32_t Y, int32_t Z, void* plan) {
+  g_err[0] = 0;
+  int st = check_ctx(ctx);
+  if (st) return st;
+  if (N < 0 || N > INT32_MAX - 64)
+    return fail(TSC_ERR_INVALID, "map_gather_plan: N=%lld out of range", (long long)N);
+  if (B <= 0 || X <= 0 || Y <= 0 || Z <= 0)
+    return fail(TSC_ERR_INVALID, "map_gather_plan: grid %dx%dx%dx%d must be positive", B, X, Y, Z);
+  if (N > 0 && (!coords || !nbr || !plan))
+    return fail(TSC_ERR_INVALID, "map_gather_plan: null coords/nbr/plan");
+  if (coords && !aligned(coords, 16))
+    return fail(TSC_ERR_INVALID, "map_gather_plan: coords must be 16-byte aligned");
+  if (plan && !aligned(plan, 256))
+    return fail(TSC_ERR_INVALID, "map_gather_plan: plan must be 256-byte aligned");
+  DeviceGuard g(ctx->device);
+  return tsc::gather_plan_launch(ctx, coords, nbr, N, B, X, Y, Z, plan);
+}
+
+int tsc_conv_planned(tsc_ctx* ctx, int32_t dtype, const void* feats, const void* weight,
+                     const void* bias, const int32_t* nbr, const void* plan, int64_t N,
+                     int32_t Ci, int32_t Co, int32_t epilogue, const void* residual,
+                     const void* ln_gamma, const void* ln_beta, float eps, void* out) {
+  g_err[0] = 0;
+  int st = validate_conv(ctx, dtype, feats, weight, bias, nbr, N, Ci, Co, out);
+  if (st) return st;
+  if (epilogue < TSC_EPI_BIAS || epilogue > TSC_EPI_BIAS_LN_SILU)
+    return fail(TSC_ERR_INVALID, "conv: unknown epilogue %d", epilogue);
+  if (epilogue == TSC_EPI_BIAS_RESIDUAL && N > 0 && !residual)
+    return fail(TSC_ERR_INVALID, "conv: residual epilogue needs a residual buffer");
+  if (N > 0 && !plan) return fail(TSC_ERR_INVALID, "conv_planned: null plan");
+  if (plan && !aligned(plan, 256))
+    return fail(TSC_ERR_INVALID, "conv_planned: plan must be 256-byte aligned");
+  if (N == 0) return TSC_OK;
+  if (N > INT32_MAX - 64)
+    return fail(TSC_ERR_INVALID, "conv_planned: N=%lld out of range", (long long)N);
+  DeviceGuard g(ctx->device);
+  ConvArgs a{dtype, feats, weight, bias, nbr, nullptr, N, Ci, Co,
+             epilogue == TSC_EPI_BIAS_RESIDUAL ? TSC_EPI_BIAS_RESIDUAL : TSC_EPI_BIAS,
+             residual, out, plan};
+  st = conv_launch(ctx, a);
+  if (st || epilogue != TSC_EPI_BIAS_LN_SILU) return st;
+  return layernorm_launch(ctx, dtype, out, N, Co, ln_gamma, ln_beta, eps, 1, out);
+}
+
 int tsc_conv(tsc_ctx* ctx, int32_t dtype, const void* feats, const void* weight, const void* bias,
              const int32_t* nbr, const int32_t* order, int64_t N, int32_t Ci, int32_t Co,
              void* out) {

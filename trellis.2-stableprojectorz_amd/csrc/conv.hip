@@ -1090,6 +1090,13 @@ int dispatch_epi(tsc_ctx* ctx, const ConvArgs& a) {
 
 int conv_launch(tsc_ctx* ctx, const ConvArgs& a) {
   if (a.N == 0) return TSC_OK;
+  if (conv_gather_supported(a)) return conv_gather_launch(ctx, a);
+  if (a.plan && !a.order) {  // other shapes: the plan's Morton row order
+    ConvArgs b = a;
+    b.order = (const int32_t*)((const char*)a.plan + plan_layout(a.N).rows);
+    b.plan = nullptr;
+    return conv_launch(ctx, b);
+  }
   switch (a.dtype) {
     case TSC_F32: return dispatch_epi<float>(ctx, a);
     case TSC_F16: return dispatch_epi<_Float16>(ctx, a);

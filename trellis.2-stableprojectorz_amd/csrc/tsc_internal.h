@@ -115,8 +115,23 @@ struct ConvArgs {
   int32_t epilogue;      // TSC_EPI_BIAS or TSC_EPI_BIAS_RESIDUAL (LN handled by the caller)
   const void* residual;  // for TSC_EPI_BIAS_RESIDUAL
   void* out;
+  const void* plan = nullptr;  // gather plan (conv_gather.hip) or null
 };
 int conv_launch(tsc_ctx* ctx, const ConvArgs& a);
+
+// ---- gather plan + planned narrow conv (conv_gather.hip) ----
+constexpr int kPlanRows = 64;                   // rows per plan tile
+constexpr int kPlanSlots = 256;                 // distinct-row list capacity per tile
+constexpr int kPlanTableBytes = 16 * 28 * 4;    // slot table per tile: [16][28 taps][4 blocks]
+struct PlanLayout {
+  int64_t T;                                    // tiles
+  size_t rows, count, rbm, list, slots, total;  // byte offsets in the plan buffer, and its size
+};
+PlanLayout plan_layout(int64_t N);
+int gather_plan_launch(tsc_ctx* ctx, const int32_t* coords, const int32_t* nbr, int64_t N,
+                       int32_t B, int32_t X, int32_t Y, int32_t Z, void* plan);
+bool conv_gather_supported(const ConvArgs& a);
+int conv_gather_launch(tsc_ctx* ctx, const ConvArgs& a);
 
 // ---- launchers implemented in subdivide.hip ----
 int subdivide_count_launch(tsc_ctx* ctx, const uint8_t* keep, int64_t N, int64_t* count_host);

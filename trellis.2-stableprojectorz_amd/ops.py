@@ -53,13 +53,24 @@ class NeighborMap:
     spatial_shape: tuple
     batch_size: int
     dilation: tuple
+    coords: torch.Tensor | None = None  # the (N,4) input, kept for the gather plan
     _conv_order: torch.Tensor | None = None
+    _gather_plan: torch.Tensor | None = None
 
     def conv_order(self) -> torch.Tensor:
         """Row order the convs use (tsc_map_conv_order), computed on first use and cached."""
         if self._conv_order is None:
             self._conv_order = map_conv_order(self.nbr, self.perm)
         return self._conv_order
+
+    def gather_plan(self) -> torch.Tensor:
+        """Gather plan of the narrow convs (tsc_map_gather_plan), computed on first use and cached."""
+        if self._gather_plan is None:
+            if self.coords is None:
+                raise TscError(_lib.TSC_ERR_INVALID, "gather plan needs the map's coords")
+            self._gather_plan = map_gather_plan(self.coords, self.nbr, self.batch_size,
+                                                self.spatial_shape)
+        return self._gather_plan
 
 
 def map_conv_order(nbr: torch.Tensor, perm: torch.Tensor | None = None) -> torch.Tensor:
@@ -74,6 +85,26 @@ def map_conv_order(nbr: torch.Tensor, perm: torch.Tensor | None = None) -> torch
     order = torch.empty((n,), dtype=torch.int32, device=nbr.device)
     check(ctx.lib.tsc_map_conv_order(ctx.bind(), _p(nbr), _p(perm), n, _p(order)))
     return order
+
+
+def map_gather_plan(coords: torch.Tensor, nbr: torch.Tensor, batch_size: int,
+                    spatial_shape) -> torch.Tensor:
+    """Gather plan (uint8 device buffer) of the narrow convs over this coordinate set and map."""
+    if coords.dtype != torch.int32 or coords.dim() != 2 or coords.shape[1] != 4:
+        raise TscError(_lib.TSC_ERR_INVALID, "coords must be int32 of shape (N,4)")
+    n = coords.shape[0]
+    if nbr.dtype != torch.int32 or tuple(nbr.shape) != (n, 27):
+        raise TscError(_lib.TSC_ERR_INVALID, "nbr must be int32 (N,27)")
+    dev = _dev(coords, nbr)
+    ctx = _lib.context(dev)
+    nbytes = ctx.lib.tsc_map_gather_plan_bytes(n)
+    if nbytes < 0:
+        raise TscError(_lib.TSC_ERR_INVALID, f"gather plan: N={n} out of range")
+    plan = torch.empty((max(nbytes, 1),), dtype=torch.uint8, device=coords.device)
+    X, Y, Z = (int(s) for s in spatial_shape)
+    check(ctx.lib.tsc_map_gather_plan(ctx.bind(), _p(coords), _p(nbr), n, int(batch_size), X, Y, Z,
+                                      _p(plan)))
+    return plan
 
 
 def build_neighbor_map(coords: torch.Tensor, spatial_shape, batch_size: int,
@@ -111,7 +142,7 @@ def build_neighbor_map(coords: torch.Tensor, spatial_shape, batch_size: int,
             if st & _lib.TSC_MAP_OUT_OF_RANGE:
                 what.append(f"coordinates outside [0,{batch_size})x[0,{X})x[0,{Y})x[0,{Z})")
             raise TscError(_lib.TSC_ERR_INVALID, "map build: " + ", ".join(what))
-    return NeighborMap(nbr, keys, perm, (X, Y, Z), int(batch_size), tuple(dilation))
+    return NeighborMap(nbr, keys, perm, (X, Y, Z), int(batch_size), tuple(dilation), coords)
 
 
 def _nbr_and_order(nmap, order):
@@ -120,15 +151,25 @@ def _nbr_and_order(nmap, order):
     return nmap, order
 
 
+def _uses_gather_plan(nmap, order, feats, weight) -> bool:
+    """Narrow 16-bit convs (Ci = 32, Co = 32/64) on a NeighborMap without an explicit order."""
+    if not isinstance(nmap, NeighborMap) or order is not None or nmap.coords is None:
+        return False
+    return (feats.dtype in (torch.float16, torch.bfloat16) and weight.dim() == 5
+            and weight.shape[4] == 32 and weight.shape[0] in (32, 64))
+
+
 def sparse_conv3d(feats: torch.Tensor, weight: torch.Tensor, bias, nmap, order=None,
                   epilogue: str = "bias", residual=None, ln_weight=None, ln_bias=None,
                   eps: float = 1e-6, out=None) -> torch.Tensor:
     """out = bias + sum_v feats[nbr[:,v]] @ W[:,v,:]^T  (+ residual | -> LN -> SiLU).
 
     weight is (Co,Kd,Kh,Kw,Ci) = (Co,3,3,3,Ci), same dtype as feats; accumulation is fp32.
-    nmap is a NeighborMap (its sorted order is used for locality) or an (N,27) int32 table.
+    nmap is a NeighborMap (its cached row order, or for Ci = 32 in fp16/bf16 its cached gather
+    plan, is used for locality) or an (N,27) int32 table.
     """
-    nbr, order = _nbr_and_order(nmap, order)
+    plan = nmap.gather_plan() if _uses_gather_plan(nmap, order, feats, weight) else None
+    nbr, order = (nmap.nbr, None) if plan is not None else _nbr_and_order(nmap, order)
     if weight.dim() != 5 or tuple(weight.shape[1:4]) != (3, 3, 3):
         raise TscError(_lib.TSC_ERR_UNSUPPORTED, f"weight must be (Co,3,3,3,Ci), got {tuple(weight.shape)}")
     co, ci = weight.shape[0], weight.shape[4]
@@ -152,6 +193,11 @@ def sparse_conv3d(feats: torch.Tensor, weight: torch.Tensor, bias, nmap, order=N
     if out is None:
         out = torch.empty((n, co), dtype=feats.dtype, device=feats.device)
     ctx = _lib.context(dev)
+    if plan is not None:
+        check(ctx.lib.tsc_conv_planned(ctx.bind(), _code(feats), _p(feats), _p(weight), _p(bias),
+                                       _p(nbr), _p(plan), n, ci, co, epi, _p(residual), _p(ln_weight),
+                                       _p(ln_bias), float(eps), _p(out)))
+        return out
     check(ctx.lib.tsc_conv_fused(ctx.bind(), _code(feats), _p(feats), _p(weight), _p(bias), _p(nbr),
                                  _p(order), n, ci, co, epi, _p(residual), _p(ln_weight), _p(ln_bias),
                                  float(eps), _p(out)))
