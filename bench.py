@@ -514,6 +514,9 @@ def main() -> int:
     # One-time per coordinate set, cached with the map: the row order the convs use.
     order_ms = time_steps(lambda: pkg.map_conv_order(nmap.nbr, nmap.perm), args.steps, args.warmup)
     log(f"conv row order (tsc_map_conv_order): {order_ms:.4f} ms")
+    plan_ms = time_steps(lambda: pkg.map_gather_plan(c_dev, nmap.nbr, 1, shape), args.steps,
+                         args.warmup)
+    log(f"narrow-conv gather plan (tsc_map_gather_plan): {plan_ms:.4f} ms")
     del nmap
     sec = []
     if not args.no_secondary:
@@ -537,9 +540,9 @@ def main() -> int:
                    "voxels": n, "grid": list(shape), "batch": 1,
                    "bytes_per_voxel_algorithmic": MAP_BYTES_PER_VOXEL},
         "roofline": roofline, "cpu_baseline": cpu,
-        "map_prep": {"conv_order_ms": round(order_ms, 4),
-                     "note": "tsc_map_conv_order, once per coordinate set (cached with the map); "
-                             "not part of ms_per_step"},
+        "map_prep": {"conv_order_ms": round(order_ms, 4), "gather_plan_ms": round(plan_ms, 4),
+                     "note": "tsc_map_conv_order and tsc_map_gather_plan, once per coordinate set "
+                             "(cached with the map); not part of ms_per_step"},
         "secondary": sec,
     }
     print(json.dumps(line), flush=True)

@@ -17,7 +17,8 @@ is not a Python identifier.
 from ._lib import TscError, load_library, header_symbols, LIB_PATH  # noqa: F401
 from .sparse_tensor import SparseTensor, Scale, Fraction, SCALE_IDENTITY, compute_layout  # noqa: F401
 from .conv3d import SparseConv3d, SparseResBlock3d, get_neighbor_map, neighbor_cache_key  # noqa: F401
-from .ops import (NeighborMap, build_neighbor_map, map_conv_order, sparse_conv3d,  # noqa: F401
+from .ops import (NeighborMap, build_neighbor_map, map_conv_order, map_gather_plan,  # noqa: F401
+                  sparse_conv3d,
                   layer_norm, silu, add, sparse_resblock, sparse_subdivide, subdivide_count,
                   sparse_linear, sparse_attention, scaled_dot_product_attention)
 from .spatial import SparseSubdivide  # noqa: F401
@@ -27,7 +28,7 @@ from . import workloads  # noqa: F401
 
 __all__ = [
     "TscError", "SparseTensor", "SparseConv3d", "SparseResBlock3d", "NeighborMap",
-    "build_neighbor_map", "map_conv_order", "sparse_conv3d", "layer_norm", "silu", "add", "sparse_resblock",
+    "build_neighbor_map", "map_conv_order", "map_gather_plan", "sparse_conv3d", "layer_norm", "silu", "add", "sparse_resblock",
     "sparse_subdivide", "subdivide_count", "SparseSubdivide", "sparse_linear", "SparseLinear",
     "SparseConvNeXtBlock3d", "sparse_attention", "scaled_dot_product_attention", "SafetensorsFile", "SafetensorsHeader", "TensorEntry", "MultiFileLoader",
     "get_neighbor_map", "neighbor_cache_key", "workloads",
