@@ -28,6 +28,8 @@ def _conv_name(kind: str, t: str, nums: list) -> str:
     if kind == "conv_mfma_kernel":  # BM, BN, KB, STAGES, WM, WN, EPI
         bm, bn, kb, st, _, _, epi = nums
         return f"conv_mfma_kernel<{t},{bm}x{bn},k{kb},s{st}{',res' if epi == '1' else ''}>"
+    if kind == "conv_gather_kernel":  # EPI
+        return f"conv_gather_kernel<{t}{',res' if nums[0] == '1' else ''}>"
     if kind == "conv_narrow_kernel":  # CO, EPI, threads
         co, epi, _ = nums
         return f"conv_narrow_kernel<{t},32x{co}{',res' if epi == '1' else ''}>"
@@ -36,7 +38,7 @@ def _conv_name(kind: str, t: str, nums: list) -> str:
 
 
 def short_name(name: str) -> str:
-    kinds = "conv_mfma_kernel|conv_regstage_kernel|conv_narrow_kernel"
+    kinds = "conv_mfma_kernel|conv_regstage_kernel|conv_narrow_kernel|conv_gather_kernel"
     m = re.search(rf"({kinds})I(DF16b|DF16_|f)((?:Li\d+E)+)", name)  # mangled
     if m:
         return _conv_name(m.group(1), _TYPES[m.group(2)], re.findall(r"Li(\d+)E", m.group(3)))
