@@ -58,7 +58,8 @@ typedef __bf16 bf16x8_t __attribute__((__vector_size__(8 * sizeof(__bf16))));
 typedef float f32x4_t __attribute__((__vector_size__(4 * sizeof(float))));
 
 constexpr int kTaps = 27;
-constexpr int kHash = 2048;        // per-tile hash capacity (> 64 * 27 entries)
+constexpr int kHash = 512;         // per-tile hash capacity (tiles past 255 rows overflow)
+constexpr int kHashShift = 23;     // 32 - log2(kHash)
 constexpr int kPrioWords = 56;     // 1792 priorities / 32
 constexpr int kPlanWaves = 4;
 constexpr int kTableQ = kPlanTableBytes / 16;  // 112 uint4 per tile table
@@ -89,8 +90,8 @@ __global__ void __launch_bounds__(64 * kPlanWaves)
                      int64_t N, int64_t T, int32_t* __restrict__ rows_out,
                      int32_t* __restrict__ count_out, uint32_t* __restrict__ rbm_out,
                      int32_t* __restrict__ list_out, uint4* __restrict__ slots_out) {
-  __shared__ int32_t hkey[kPlanWaves][kHash];
-  __shared__ int32_t hval[kPlanWaves][kHash];  // min priority, then slot
+  __shared__ __attribute__((aligned(16))) int32_t hkey[kPlanWaves][kHash];
+  __shared__ __attribute__((aligned(16))) int32_t hval[kPlanWaves][kHash];  // min prio, then slot
   __shared__ uint32_t pbits[kPlanWaves][kPrioWords];
   __shared__ int32_t ppre[kPlanWaves][64];
   __shared__ uint4 table[kPlanWaves][kTableQ];
@@ -99,9 +100,9 @@ __global__ void __launch_bounds__(64 * kPlanWaves)
   if (t >= T) return;  // whole wave
   int32_t* const hk = hkey[w];
   int32_t* const hv = hval[w];
-  for (int i = lane; i < kHash; i += 64) {
-    hk[i] = -1;
-    hv[i] = INT_MAX;
+  for (int i = lane; i < kHash / 4; i += 64) {  // 16-byte stores
+    ((int4*)hk)[i] = make_int4(-1, -1, -1, -1);
+    ((int4*)hv)[i] = make_int4(INT_MAX, INT_MAX, INT_MAX, INT_MAX);
   }
   if (lane < kPrioWords) pbits[w][lane] = 0u;
   for (int i = lane; i < kTableQ; i += 64) table[w][i] = make_uint4(0, 0, 0, 0);
@@ -113,37 +114,56 @@ __global__ void __launch_bounds__(64 * kPlanWaves)
   const int32_t row = pos < N ? sorted_rows[pos] : -1;
   rows_out[pos] = row;
   // Insert every present neighbor with priority: own row (tap 13) = its position in the tile,
-  // else 64 + 64*tap + position.  Linear probing; capacity exceeds the 1728 possible entries.
+  // else 64 + 64*tap + position.  Linear probing; an insert that finds the table full marks the
+  // tile as overflowing (it has more distinct rows than a list holds anyway).
+  // All 27 entries are loaded before the first insert, so the loads overlap.
+  int32_t ev[kTaps];
+#pragma unroll
+  for (int v = 0; v < kTaps; ++v) ev[v] = row >= 0 ? nbr[(int64_t)row * kTaps + v] : -1;
   int hpos[kTaps];
   uint32_t present = 0;
+  bool full = false;
 #pragma unroll
   for (int v = 0; v < kTaps; ++v) {
-    const int32_t e = row >= 0 ? nbr[(int64_t)row * kTaps + v] : -1;
+    const int32_t e = ev[v];
     hpos[v] = -1;
     if (e >= 0) {
       present |= 1u << v;
       const int prio = v == 13 ? lane : 64 + 64 * v + lane;
-      int h = (int)(((uint32_t)e * 2654435761u) >> 21);
-      for (;;) {
+      int h = (int)(((uint32_t)e * 2654435761u) >> kHashShift);
+      bool ok = false;
+      for (int probe = 0; probe < kHash; ++probe) {
         const int32_t old = atomicCAS(&hk[h], -1, e);
-        if (old == -1 || old == e) break;
+        if (old == -1 || old == e) {
+          ok = true;
+          break;
+        }
         h = (h + 1) & (kHash - 1);
       }
-      atomicMin(&hv[h], prio);
-      hpos[v] = h;
+      if (ok) {
+        atomicMin(&hv[h], prio);
+        hpos[v] = h;
+      } else {
+        full = true;
+      }
     }
   }
+  const bool overflow = __ballot(full) != 0;
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
   // Distinct count and the set of their (distinct) minimum priorities.
   int cnt = 0;
-  for (int i = lane; i < kHash; i += 64) {
-    if (hk[i] >= 0) {
-      ++cnt;
-      const int p = hv[i];
-      atomicOr(&pbits[w][p >> 5], 1u << (p & 31));
-    }
+  for (int i = lane; i < kHash / 4; i += 64) {
+    const int4 k4 = ((const int4*)hk)[i];
+    const int4 v4 = ((const int4*)hv)[i];
+    const int kk[4] = {k4.x, k4.y, k4.z, k4.w}, vv[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (kk[u] >= 0) {
+        ++cnt;
+        atomicOr(&pbits[w][vv[u] >> 5], 1u << (vv[u] & 31));
+      }
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off, 64);
@@ -152,7 +172,7 @@ __global__ void __launch_bounds__(64 * kPlanWaves)
 #pragma unroll
   for (int off = 1; off < 16; off <<= 1) m |= __shfl_xor(m, off, 64);
   if ((lane & 15) == 0) rbm_out[t * 4 + (lane >> 4)] = m;
-  if (cnt > kPlanSlots - 1) {
+  if (overflow || cnt > kPlanSlots - 1) {
     if (lane == 0) count_out[t] = -1;
     return;
   }
@@ -174,13 +194,20 @@ __global__ void __launch_bounds__(64 * kPlanWaves)
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
   // Slot = 1 + rank of the row's minimum priority.
   int32_t* const list = list_out + t * kPlanSlots;
-  for (int i = lane; i < kHash; i += 64) {
-    if (hk[i] >= 0) {
-      const int p = hv[i];
-      const int rank = ppre[w][p >> 5] + __popc(pbits[w][p >> 5] & ((1u << (p & 31)) - 1u));
-      list[rank] = hk[i];
-      hv[i] = rank + 1;
-    }
+  for (int i = lane; i < kHash / 4; i += 64) {
+    const int4 k4 = ((const int4*)hk)[i];
+    int4 v4 = ((const int4*)hv)[i];
+    int* const vv = (int*)&v4;
+    const int kk[4] = {k4.x, k4.y, k4.z, k4.w};
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (kk[u] >= 0) {
+        const int p = vv[u];
+        const int rank = ppre[w][p >> 5] + __popc(pbits[w][p >> 5] & ((1u << (p & 31)) - 1u));
+        list[rank] = kk[u];
+        vv[u] = rank + 1;
+      }
+    ((int4*)hv)[i] = v4;
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   __builtin_amdgcn_wave_barrier();
