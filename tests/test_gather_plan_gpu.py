@@ -193,3 +193,17 @@ def test_plan_other_shapes_use_plan_order(pkg, dev):
                                             None, None, ctypes.c_float(0.0), out.data_ptr()))
     torch.cuda.synchronize()
     assert torch.equal(out, ref)
+
+
+def test_plan_64bit_morton_keys(pkg, dev):
+    """A 2048^3 grid with two samples: 34-bit Morton keys take the 64-bit sort."""
+    g = np.stack(np.meshgrid(*[np.arange(10)] * 3, indexing="ij"), -1).reshape(-1, 3)
+    xyz = np.concatenate([g + 1500, g + 37, g * 3 + 900])
+    b = np.repeat([0, 1, 1], len(g))[:, None]
+    coords = np.concatenate([b, xyz], 1).astype(np.int32)
+    coords = coords[np.random.default_rng(5).permutation(len(coords))]
+    print(f"  gather plan 2048^3 x2 N={len(coords)}", flush=True)
+    _check_plan(pkg, dev, coords, 2, (2048, 2048, 2048))
+    *_, planned, direct = _pair(pkg, dev, coords, 2, (2048, 2048, 2048), 32, 32, torch.float16,
+                                "bias")
+    assert torch.equal(planned, direct)
