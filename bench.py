@@ -361,6 +361,69 @@ def safetensors_record(pkg, steps) -> dict:
                                                f"widening (readTensorF32)"}}
 
 
+def cpu_info(threads: int) -> dict:
+    """Host facts recorded beside every CPU leg: threads used, os.cpu_count(), CPU model."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"torch_threads": threads, "os_cpu_count": os.cpu_count(), "cpu_model": model}
+
+
+def conv_cpu_baseline(f_np, w_np, nbr, dtype: str, threads: int, budget_s: float = 20.0) -> dict:
+    """The reference's conv_none restated in PyTorch-CPU (oracle/torch_path.py: per tap
+    index_select of the valid neighbor rows -> mm with W[:,v,:]^T -> index_add), timed on this
+    host: median of up to 3 runs after one warm-up, fewer when a run takes long (wall-clock).
+    fp16 / bf16 inputs are rounded to that type and computed in fp32 (torch's CPU half matmuls
+    are not a fair baseline)."""
+    import torch
+
+    from oracle import torch_path
+
+    dts = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16}
+    torch.set_num_threads(threads)
+    f = torch.from_numpy(f_np).to(dts[dtype]).float()
+    w = torch.from_numpy(w_np).to(dts[dtype]).float()
+    nb = nbr.cpu() if hasattr(nbr, "cpu") else torch.from_numpy(nbr)
+    times = []
+    t_all = time.perf_counter()
+    warm = True
+    while len(times) < 3:
+        t0 = time.perf_counter()
+        torch_path.conv_none(f, w, None, nb, acc_dtype=torch.float32)
+        dt = time.perf_counter() - t0
+        if warm and dt < 2.0:  # short runs: the first one is a warm-up
+            warm = False
+            continue
+        warm = False
+        times.append(dt)
+        if time.perf_counter() - t_all > budget_s:
+            break
+    t = statistics.median(times)
+    rec = {"value": round(t * 1e3, 2), "unit": "ms/conv", "cores": threads, "kind": "port",
+           "runs": len(times),
+           "sample": f"full conv, conv_none restated in torch {torch.__version__} on the CPU "
+                     f"(fp32 compute{'' if dtype == 'float32' else ' on ' + dtype + '-rounded inputs'})"}
+    rec.update(cpu_info(threads))
+    return rec
+
+
+def load_counters():
+    """Per-kernel rocprofv3 counter averages (profiles/mfma_counters.json), or {}."""
+    p = ROOT / "profiles" / "mfma_counters.json"
+    if not p.exists():
+        return {}
+    try:
+        return json.loads(p.read_text()).get("kernels", {})
+    except ValueError:
+        return {}
+
+
 def cpu_baseline(coords_np, shape, threads: int) -> dict:
     import torch
 
@@ -376,10 +439,12 @@ def cpu_baseline(coords_np, shape, threads: int) -> dict:
         torch_path.hashmap_fallback(c, shape)
         times.append(time.perf_counter() - t0)
     t = statistics.median(times)
-    return {"value": round(MAP_BYTES_PER_VOXEL * n / t / 1e9, 4), "unit": "GB/s", "cores": threads,
-            "kind": "port", "ms": round(t * 1e3, 2),
-            "sample": f"full map512 coordinate set (N={n}), torch.sort + 27 torch.searchsorted, "
-                      f"median of 3 after a warm-up, torch {torch.__version__}"}
+    rec = {"value": round(MAP_BYTES_PER_VOXEL * n / t / 1e9, 4), "unit": "GB/s", "cores": threads,
+           "kind": "port", "ms": round(t * 1e3, 2),
+           "sample": f"full map512 coordinate set (N={n}), torch.sort + 27 torch.searchsorted, "
+                     f"median of 3 after a warm-up, torch {torch.__version__}"}
+    rec.update(cpu_info(threads))
+    return rec
 
 
 def conv_record(name, ms, n, p, ci, co, dtype, extra=None) -> dict:
@@ -399,11 +464,29 @@ def conv_record(name, ms, n, p, ci, co, dtype, extra=None) -> dict:
     return rec
 
 
-def secondary(pkg, dev, steps, warmup, map512_coords) -> list:
+def attach_counters(rec: dict, counters: dict, flops: float | None = None) -> None:
+    """Add the rocprofv3 counter figures of the record's kernels (profiles/mfma_counters.json)."""
+    got = {}
+    for k in rec.get("kernels", {}):
+        c = counters.get(k)
+        if not c:
+            continue
+        e = {key: round(c[key], 4) for key in ("mfma_busy", "mfma_tflops_hw", "avg_us") if key in c}
+        if flops and c.get("avg_us") and c.get("mfma_tflops_hw"):
+            # executed MFMA work over valid-tap work: > 1 means zero-padded taps were computed
+            e["mfma_work_over_algorithmic"] = round(c["mfma_tflops_hw"] * 1e12 * c["avg_us"] * 1e-6
+                                                    / flops, 3)
+        got[k] = e
+    if got:
+        rec["counters"] = {"source": "profiles/mfma_counters.txt", "kernels": got}
+
+
+def secondary(pkg, dev, steps, warmup, map512_coords, cpu_threads=None) -> list:
     import numpy as np
     import torch
 
     wl = pkg.workloads
+    counters = load_counters()
     out = []
     dts = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16}
     for name in ("conv64_f32", "narrow512_f16", "wide128_bf16", "resblock64_bf16"):
@@ -445,6 +528,13 @@ def secondary(pkg, dev, steps, warmup, map512_coords) -> list:
                 rec = conv_record(name, ms, n, p, ci, co, w.dtype)
                 kt = kernel_times(pkg._lib.context(dev.index), conv, 3)
             rec["kernels"] = {k: {"avg_ms": round(a, 4), "launches_per_step": c} for k, (a, c) in kt.items()}
+            attach_counters(rec, counters, 2.0 * p * ci * co)
+            if cpu_threads:
+                log(f"{name} {ci}->{co}: CPU conv_none baseline on {cpu_threads} threads ...")
+                rec["cpu_baseline"] = conv_cpu_baseline(wl.features(n, ci, 1),
+                                                        wl.conv_weight(co, ci, 2), nmap.nbr,
+                                                        w.dtype, cpu_threads)
+                log(f"  cpu: {rec['cpu_baseline']['value']} ms/conv")
             out.append(rec)
             log(f"{name} {ci}->{co} {w.dtype}: {rec['ms_per_conv']} ms/conv, "
                 f"{rec['tflops_effective']} TFLOP/s eff, {rec['gbps_algorithmic']} GB/s, "
@@ -520,7 +610,8 @@ def main() -> int:
     del nmap
     sec = []
     if not args.no_secondary:
-        sec = secondary(pkg, dev, args.steps, args.warmup, coords)
+        sec = secondary(pkg, dev, args.steps, args.warmup, coords,
+                        None if args.no_cpu_baseline else args.cpu_threads)
         sec += subdivide_records(pkg, dev, args.steps, args.warmup)
         sec.append(convnext_record(pkg, dev, args.steps, args.warmup))
         sec.append(attention_record(pkg, dev, args.steps))
@@ -541,8 +632,12 @@ def main() -> int:
                    "bytes_per_voxel_algorithmic": MAP_BYTES_PER_VOXEL},
         "roofline": roofline, "cpu_baseline": cpu,
         "map_prep": {"conv_order_ms": round(order_ms, 4), "gather_plan_ms": round(plan_ms, 4),
+                     "map_ready_ms": round(ms + order_ms, 4),
+                     "map_ready_narrow_ms": round(ms + plan_ms, 4),
                      "note": "tsc_map_conv_order and tsc_map_gather_plan, once per coordinate set "
-                             "(cached with the map); not part of ms_per_step"},
+                             "(cached with the map); not part of ms_per_step.  map_ready = build + "
+                             "row order (what a wide conv needs first), map_ready_narrow = build + "
+                             "gather plan (what a narrow 16-bit conv needs first)"},
         "secondary": sec,
     }
     print(json.dumps(line), flush=True)

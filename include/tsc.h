@@ -135,11 +135,16 @@ int tsc_map_gather_plan(tsc_ctx* ctx, const int32_t* coords, const int32_t* nbr,
 
 /* ---- convolution -------------------------------------------------------------------------- */
 /* out[n,co] = bias[co] + sum_{v: nbr[n,v]>=0} sum_ci feats[nbr[n,v],ci] * W[co,v,ci]
- *   feats (N,Ci), weight (Co,3,3,3,Ci), bias (Co) or NULL, out (N,Co): all `dtype`, row-major.
+ *   feats (N,Ci), weight (Co,3,3,3,Ci), bias (Co) or NULL, out (N,Co): all `dtype`, row-major,
+ *   each aligned to its element size; nbr 4-byte aligned.
  *   order: optional device int32 (N) permutation; rows are processed in that order (pass
  *   tsc_map_conv_order's output, or the map's perm_out for spatial locality).  NULL = 0..N-1.
  *   Results do not depend on it.
- * Replaces conv3d.ts:154-221 / conv3d_wgsl.ts:132-231.  Ci and Co must be multiples of 16. */
+ *   Any Ci >= 1 (Ci * element size <= 65536 bytes) and 1 <= Co <= 65536, as the reference's
+ *   bounds-checked shader (conv3d_wgsl.ts:174-196).  The tuned kernels run when Ci * element size
+ *   is a multiple of 32 bytes, Co a multiple of 32 and every buffer 16-byte aligned; other
+ *   shapes run a generic kernel (zero-padded K tail, masked Co tail), with the same arithmetic.
+ * Replaces conv3d.ts:154-221 / conv3d_wgsl.ts:132-231. */
 int tsc_conv(tsc_ctx* ctx, int32_t dtype, const void* feats, const void* weight, const void* bias,
              const int32_t* nbr, const int32_t* order, int64_t N, int32_t Ci, int32_t Co, void* out);
 

@@ -47,7 +47,7 @@ def conv_none(feats: torch.Tensor, weight: torch.Tensor, bias, nbr: torch.Tensor
     """out = bias + sum_v feats[nbr[:,v]] @ W[:,v,:]^T over valid taps, accumulated in acc_dtype."""
     co, ci = weight.shape[0], weight.shape[-1]
     w = weight.reshape(co, 27, ci).to(acc_dtype)
-    out = torch.zeros(feats.shape[0], co, dtype=acc_dtype)
+    out = torch.zeros(nbr.shape[0], co, dtype=acc_dtype, device=feats.device)
     f = feats.to(acc_dtype)
     for v in range(27):
         idx = nbr[:, v].to(torch.int64)

@@ -111,9 +111,8 @@ def test_conv_bf16_wide_full_size(pkg, dev):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("ci,co", [(16, 32), (64, 128), (96, 96), (128, 256), (256, 64)])
 def test_conv_dtypes_and_shapes(pkg, dev, dtype, ci, co):
-    if dtype == torch.float32 or ci * 2 % 32 == 0:
-        err, *_ = _workload_conv(pkg, dev, "resblock64_bf16", ci, co, dtype, sample_rows=800)
-        assert err <= TOL[dtype], err
+    err, *_ = _workload_conv(pkg, dev, "resblock64_bf16", ci, co, dtype, sample_rows=800)
+    assert err <= TOL[dtype], err
 
 
 @pytest.mark.parametrize("ci,co,rows", [(64, 768, None), (64, 256, 100), (128, 512, 2000)])
@@ -231,16 +230,81 @@ def test_conv_epilogues(pkg, dev):
     assert rel_err(r2.float().cpu().numpy(), base + r64) <= 2e-2
 
 
-def test_conv_rejects_unsupported(pkg, dev):
+def _small_map(pkg, dev, n_keep=3000):
+    coords = pkg.workloads.make_coords("conv64_f32")[:n_keep]
+    return coords, _map(pkg, dev, coords, 1, (64, 64, 64))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("ci,co", [(1, 1), (3, 7), (13, 48), (40, 72), (8, 32), (32, 48),
+                                   (24, 100)])
+def test_conv_any_channels(pkg, dev, dtype, ci, co):
+    """Channel counts the tuned kernels do not take (rows not a multiple of 32 bytes, Co not a
+    multiple of 32) run the generic kernel: zero-padded K tail, masked Co tail.  The reference
+    shader accepts any Ci and Co (conv3d_wgsl.ts:174-196)."""
+    coords, m = _small_map(pkg, dev)
+    n = len(coords)
+    nbr = m.nbr.cpu().numpy()
+    print(f"  conv any channels N={n} {ci}->{co} {dtype}", flush=True)
+    f, f64 = _rounded(pkg.workloads.features(n, ci, ci), dtype, dev)
+    w, w64 = _rounded(pkg.workloads.conv_weight(co, ci, co), dtype, dev)
+    b, b64 = _rounded(np.linspace(-0.5, 0.5, co).astype(np.float32), dtype, dev)
+    out = pkg.sparse_conv3d(f, w, b, m).float().cpu().numpy()
+    assert rel_err(out, oracle.conv(f64, w64, b64, nbr)) <= TOL[dtype]
+    r, r64 = _rounded(pkg.workloads.features(n, co, 7), dtype, dev)
+    out = pkg.sparse_conv3d(f, w, None, m, epilogue="residual", residual=r).float().cpu().numpy()
+    assert rel_err(out, oracle.conv(f64, w64, None, nbr) + r64) <= TOL[dtype]
+    g, g64 = _rounded(np.linspace(0.5, 1.5, co).astype(np.float32), dtype, dev)
+    out = pkg.sparse_conv3d(f, w, b, m, epilogue="ln_silu", ln_weight=g, eps=1e-6)
+    ref = oracle.layernorm(oracle.conv(f64, w64, b64, nbr), g64, None, 1e-6, silu=True)
+    assert rel_err(out.float().cpu().numpy(), ref) <= TOL[dtype] * (2 if co < 8 else 1)
+
+
+def _offset(t: torch.Tensor) -> torch.Tensor:
+    """A contiguous copy of t whose data pointer is one element past a 256-byte boundary."""
+    buf = torch.empty(t.numel() + 1, dtype=t.dtype, device=t.device)
+    v = buf[1:].view(t.shape)
+    v.copy_(t)
+    assert v.data_ptr() % 16 != 0
+    return v
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_conv_misaligned_buffers_take_generic_kernel(pkg, dev, dtype):
+    """Buffers aligned only to their element size run the generic kernel (element stores), with
+    the same bits as the tuned kernels on aligned buffers: both accumulate every row's taps in
+    ascending order and each tap's channels in the same MFMA K groups."""
+    coords, m = _small_map(pkg, dev)
+    n = len(coords)
+    f = torch.from_numpy(pkg.workloads.features(n, 64, 3)).to(dev).to(dtype)
+    w = torch.from_numpy(pkg.workloads.conv_weight(64, 64, 4)).to(dev).to(dtype)
+    b = torch.linspace(-1, 1, 64, device=dev).to(dtype)
+    r = torch.from_numpy(pkg.workloads.features(n, 64, 5)).to(dev).to(dtype)
+    print(f"  conv misaligned N={n} {dtype}", flush=True)
+    want = pkg.sparse_conv3d(f, w, b, m.nbr, epilogue="residual", residual=r)
+    fo, wo, bo, ro = _offset(f), _offset(w), _offset(b), _offset(r)
+    out = _offset(torch.zeros_like(want))
+    pkg.sparse_conv3d(fo, wo, bo, m.nbr, epilogue="residual", residual=ro, out=out)
+    assert torch.equal(out, want)
+    nbr = m.nbr.cpu().numpy()
+    ref = oracle.conv(f.float().cpu().numpy(), w.float().cpu().numpy(), b.float().cpu().numpy(), nbr)
+    assert rel_err(out.float().cpu().numpy(), ref + r.float().cpu().numpy()) <= TOL[dtype]
+
+
+def test_conv_rejects_invalid(pkg, dev):
     coords = np.array([[0, 1, 1, 1]], np.int32)
     m = _map(pkg, dev, coords, 1, (3, 3, 3))
-    f = torch.zeros((1, 8), device=dev, dtype=torch.float16)
-    w = torch.zeros((32, 3, 3, 3, 8), device=dev, dtype=torch.float16)
-    with pytest.raises(pkg.TscError, match="multiple of 32"):
-        pkg.sparse_conv3d(f, w, None, m)  # 8 fp16 channels = 16 bytes
     f = torch.zeros((1, 32), device=dev, dtype=torch.float16)
     w = torch.zeros((48, 3, 3, 3, 32), device=dev, dtype=torch.float16)
-    with pytest.raises(pkg.TscError, match="Co=48"):
-        pkg.sparse_conv3d(f, w, None, m)
     with pytest.raises(pkg.TscError):
-        pkg.sparse_conv3d(f.cpu(), w[:32].cpu(), None, m)
+        pkg.sparse_conv3d(f.cpu(), w.cpu(), None, m)  # no CPU path
+    with pytest.raises(pkg.TscError):
+        pkg.sparse_conv3d(f, w.float(), None, m)  # dtype mismatch
+    with pytest.raises(pkg.TscError, match="residual"):
+        pkg.sparse_conv3d(f, w, None, m, epilogue="residual")
+    # odd byte addresses are not aligned to the 2-byte element: rejected by the C ABI
+    lib = pkg._lib.context(dev.index)
+    raw = torch.zeros(64, dtype=torch.uint8, device=dev)
+    st = lib.lib.tsc_conv(lib.bind(), pkg._lib.TSC_F16, raw.data_ptr() + 1, w.data_ptr(), None,
+                          m.nbr.data_ptr(), None, 1, 32, 48, raw.data_ptr() + 2)
+    assert st == pkg._lib.TSC_ERR_INVALID

@@ -119,15 +119,22 @@ static int validate_conv(tsc_ctx* ctx, int32_t dtype, const void* feats, const v
   if ((int64_t)Ci * es > 65536)
     return fail(TSC_ERR_UNSUPPORTED, "conv: Ci*elem_size=%lld bytes exceeds 65536",
                 (long long)Ci * es);
-  if ((Ci * es) % 32 != 0)
-    return fail(TSC_ERR_UNSUPPORTED, "conv: Ci*elem_size=%d bytes must be a multiple of 32", Ci * es);
-  if (Co % 32 != 0) return fail(TSC_ERR_UNSUPPORTED, "conv: Co=%d must be a multiple of 32", Co);
+  if (Co > 65536) return fail(TSC_ERR_UNSUPPORTED, "conv: Co=%d exceeds 65536", Co);
   if (N == 0) return TSC_OK;
   if (!feats || !weight || !nbr || !out) return fail(TSC_ERR_INVALID, "conv: null buffer");
-  if (!aligned(feats, 16) || !aligned(weight, 16))
-    return fail(TSC_ERR_INVALID, "conv: feats and weight must be 16-byte aligned");
-  if (!aligned(out, es) || (bias && !aligned(bias, es)))
-    return fail(TSC_ERR_INVALID, "conv: misaligned out/bias");
+  // Element alignment is all any kernel needs; 16-byte aligned buffers (and channel counts in
+  // whole 32-byte rows / 32-column blocks) select the tuned kernels.
+  if (!aligned(feats, es) || !aligned(weight, es) || !aligned(out, es) ||
+      (bias && !aligned(bias, es)) || !aligned(nbr, 4))
+    return fail(TSC_ERR_INVALID, "conv: feats, weight, bias and out must be aligned to their "
+                                 "element size, nbr to 4 bytes");
+  return TSC_OK;
+}
+
+static int validate_residual(int32_t dtype, const void* residual) {
+  if (!residual) return fail(TSC_ERR_INVALID, "conv: residual epilogue needs a residual buffer");
+  if (!aligned(residual, elem_size(dtype)))
+    return fail(TSC_ERR_INVALID, "conv: residual must be aligned to its element size");
   return TSC_OK;
 }
 
@@ -353,8 +360,8 @@ int tsc_conv_planned(tsc_ctx* ctx, int32_t dtype, const void* feats, const void*
   if (st) return st;
   if (epilogue < TSC_EPI_BIAS || epilogue > TSC_EPI_BIAS_LN_SILU)
     return fail(TSC_ERR_INVALID, "conv: unknown epilogue %d", epilogue);
-  if (epilogue == TSC_EPI_BIAS_RESIDUAL && N > 0 && !residual)
-    return fail(TSC_ERR_INVALID, "conv: residual epilogue needs a residual buffer");
+  if (epilogue == TSC_EPI_BIAS_RESIDUAL && N > 0 && (st = validate_residual(dtype, residual)))
+    return st;
   if (N > 0 && !plan) return fail(TSC_ERR_INVALID, "conv_planned: null plan");
   if (plan && !aligned(plan, 256))
     return fail(TSC_ERR_INVALID, "conv_planned: plan must be 256-byte aligned");
@@ -386,8 +393,8 @@ int tsc_conv_fused(tsc_ctx* ctx, int32_t dtype, const void* feats, const void* w
   if (st) return st;
   if (epilogue < TSC_EPI_BIAS || epilogue > TSC_EPI_BIAS_LN_SILU)
     return fail(TSC_ERR_INVALID, "conv: unknown epilogue %d", epilogue);
-  if (epilogue == TSC_EPI_BIAS_RESIDUAL && N > 0 && !residual)
-    return fail(TSC_ERR_INVALID, "conv: residual epilogue needs a residual buffer");
+  if (epilogue == TSC_EPI_BIAS_RESIDUAL && N > 0 && (st = validate_residual(dtype, residual)))
+    return st;
   if (N == 0) return TSC_OK;
   DeviceGuard g(ctx->device);
   ConvArgs a{dtype, feats, weight, bias, nbr, order, N, Ci, Co,
@@ -442,6 +449,11 @@ int tsc_resblock(tsc_ctx* ctx, int32_t dtype, const void* x, const int32_t* nbr,
   if (st) return st;
   if (N == 0) return TSC_OK;
   if (!w2) return fail(TSC_ERR_INVALID, "resblock: null w2");
+  const int es = elem_size(dtype);
+  if (!aligned(w2, es) || (b2 && !aligned(b2, es)) || (ln_gamma && !aligned(ln_gamma, es)) ||
+      (ln_beta && !aligned(ln_beta, es)))
+    return fail(TSC_ERR_INVALID, "resblock: w2, b2, ln_gamma and ln_beta must be aligned to "
+                                 "their element size");
   if (x == out) return fail(TSC_ERR_INVALID, "resblock: out must not alias x");
   DeviceGuard g(ctx->device);
   void* h;

@@ -688,10 +688,10 @@ int launch_reg(tsc_ctx* ctx, const ConvArgs& a) {
   const int32_t n_tiles = a.Co / BN;
   const int32_t per_xcd = tile_grid_per_xcd(m_tiles, n_tiles);
   const unsigned grid = (unsigned)per_xcd * 8u;
-  static const std::string name = std::string("conv_reg_") +
-      (sizeof(T) == 4 ? "f32" : std::is_same<T, __bf16>::value ? "bf16" : "f16") + "_" +
-      std::to_string(BM) + "x" + std::to_string(BN) + "_k" + std::to_string(KB) +
-      (EPI == TSC_EPI_BIAS_RESIDUAL ? "_res" : "");
+  static const std::string name = std::string("conv_regstage_kernel<") +
+      (sizeof(T) == 4 ? "f32" : std::is_same<T, __bf16>::value ? "bf16" : "f16") + "," +
+      std::to_string(BM) + "x" + std::to_string(BN) + ",k" + std::to_string(KB) +
+      (EPI == TSC_EPI_BIAS_RESIDUAL ? ",res>" : ">");
   ProfScope p(ctx, name.c_str());
   conv_regstage_kernel<T, BM, BN, KB, WM, WN, EPI><<<grid, 64 * WM * WN, 0, ctx->stream>>>(
       (const T*)a.feats, (const T*)a.weight, (const T*)a.bias, a.nbr, a.order, a.N, a.Ci, a.Co,
@@ -734,10 +734,10 @@ int launch_cfg(tsc_ctx* ctx, const ConvArgs& a) {
     per_xcd = per_list * n_tiles;
   }
   const unsigned grid = (unsigned)per_xcd * 8u;
-  static const std::string name = std::string("conv_") +
-      (sizeof(T) == 4 ? "f32" : std::is_same<T, __bf16>::value ? "bf16" : "f16") + "_" +
-      std::to_string(BM) + "x" + std::to_string(BN) + "_k" + std::to_string(KB) + "_s" +
-      std::to_string(STAGES) + (EPI == TSC_EPI_BIAS_RESIDUAL ? "_res" : "");
+  static const std::string name = std::string("conv_mfma_kernel<") +
+      (sizeof(T) == 4 ? "f32" : std::is_same<T, __bf16>::value ? "bf16" : "f16") + "," +
+      std::to_string(BM) + "x" + std::to_string(BN) + ",k" + std::to_string(KB) + ",s" +
+      std::to_string(STAGES) + (EPI == TSC_EPI_BIAS_RESIDUAL ? ",res>" : ">");
   ProfScope p(ctx, name.c_str());
   conv_mfma_kernel<T, BM, BN, KB, STAGES, WM, WN, EPI><<<grid, 64 * WM * WN, 0, ctx->stream>>>(
       (const T*)a.feats, (const T*)a.weight, (const T*)a.bias, a.nbr, a.order, a.N, a.Ci, a.Co,
@@ -1010,15 +1010,198 @@ int launch_narrow(tsc_ctx* ctx, const ConvArgs& a) {
   const int32_t tpx = (n_tiles + 7) / 8;
   int32_t blocks = std::min<int32_t>(256, (n_tiles + NW - 1) / NW);
   blocks = std::max<int32_t>(8, (blocks + 7) / 8 * 8);
-  static const std::string name = std::string("conv_narrow_") +
-      (std::is_same<T, __bf16>::value ? "bf16" : sizeof(T) == 4 ? "f32" : "f16") + "_32x" +
-      std::to_string(CO) +
-      (EPI == TSC_EPI_BIAS_RESIDUAL ? "_res" : "");
+  static const std::string name = std::string("conv_narrow_kernel<") +
+      (std::is_same<T, __bf16>::value ? "bf16" : sizeof(T) == 4 ? "f32" : "f16") + ",32x" +
+      std::to_string(CO) + (EPI == TSC_EPI_BIAS_RESIDUAL ? ",res>" : ">");
   ProfScope p(ctx, name.c_str());
   conv_narrow_kernel<T, CO, EPI, NT><<<blocks, NT, 0, ctx->stream>>>(
       (const T*)a.feats, (const T*)a.weight, (const T*)a.bias, a.nbr, a.order, a.N, n_tiles, tpx,
       (const T*)a.residual, (T*)a.out);
   return check_hip(hipGetLastError(), "conv launch");
+}
+
+// Any channel counts (the reference bounds-checks Ci and Co, conv3d_wgsl.ts:174-196, so it takes
+// any shape): 64-row x 64-column tiles of four 32x32 waves, K in chunks of 32 bytes per row.
+// Each chunk is loaded into registers in pieces of LW bytes (the widest width that divides the
+// row and the buffers' alignment), with pieces past Ci or past Co replaced by zeros, then stored
+// to a double-buffered LDS tile; zero pieces add exact zeros to the accumulators, so the K tail
+// needs no special case.  The epilogue stores element by element, masking columns past Co.
+// This is the path for shapes the tuned kernels do not take (row bytes not a multiple of 32,
+// Co not a multiple of 32, or buffers that are not 16-byte aligned).
+template <int LW> struct PieceOf;
+template <> struct PieceOf<2> { typedef uint16_t type; };
+template <> struct PieceOf<4> { typedef uint32_t type; };
+template <> struct PieceOf<8> { typedef uint2 type; };
+template <> struct PieceOf<16> { typedef uint4 type; };
+
+constexpr int kGenBM = 64, kGenBN = 64, kGenKB = 32, kGenThreads = 256;
+
+template <typename T, int LW, int EPI>
+__global__ void __launch_bounds__(kGenThreads)
+    conv_generic_kernel(const T* __restrict__ feats, const T* __restrict__ weight,
+                        const T* __restrict__ bias, const int32_t* __restrict__ nbr,
+                        const int32_t* __restrict__ order, int64_t N, int32_t Ci, int32_t Co,
+                        int32_t m_tiles, int32_t n_tiles, int32_t per_xcd, const T* residual,
+                        T* out) {
+  typedef typename PieceOf<LW>::type P;
+  constexpr int BM = kGenBM, BN = kGenBN, KB = kGenKB, NT = kGenThreads;
+  constexpr int EPL = LW / (int)sizeof(T);  // elements per piece
+  constexpr int KC = KB / (int)sizeof(T);   // elements per chunk
+  constexpr int LPR = KB / LW;              // pieces per row per chunk
+  constexpr int AL = BM * LPR / NT > 0 ? BM * LPR / NT : 1;
+  constexpr int BL = BN * LPR / NT > 0 ? BN * LPR / NT : 1;
+  static_assert((BM * LPR) % NT == 0 || BM * LPR < NT, "A pieces per thread");
+  __shared__ __attribute__((aligned(16))) unsigned char sA[2][BM * KB];
+  __shared__ __attribute__((aligned(16))) unsigned char sB[2][BN * KB];
+  __shared__ int32_t sNbr[BM * kTaps];
+  __shared__ int32_t sRow[BM];
+  __shared__ int32_t sTaps[kTaps];
+  __shared__ uint32_t sMask;
+
+  int m_tile, n_tile;
+  if (!tile_of(blockIdx.x, m_tiles, n_tiles, per_xcd, nullptr, &m_tile, &n_tile)) return;
+  const int64_t m0 = (int64_t)m_tile * BM;
+  const int n0 = n_tile * BN;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int wm = wid >> 1, wn = wid & 1;  // 2 x 2 waves of 32 x 32
+
+  if (tid == 0) sMask = 0u;
+  for (int r = tid; r < BM; r += NT) {
+    const int64_t pos = m0 + r;
+    sRow[r] = (pos < N) ? (order ? order[pos] : (int32_t)pos) : -1;
+  }
+  __syncthreads();
+  uint32_t mymask = 0u;
+  for (int j = tid; j < BM * kTaps; j += NT) {
+    const int r = j / kTaps, v = j - r * kTaps;
+    const int32_t row = sRow[r];
+    const int32_t s = (row >= 0) ? nbr[(int64_t)row * kTaps + v] : -1;
+    sNbr[j] = s;
+    if (s >= 0) mymask |= 1u << v;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mymask |= __shfl_xor(mymask, off, 64);
+  if (lane == 0 && mymask) atomicOr(&sMask, mymask);
+  __syncthreads();
+  const uint32_t mask = sMask;
+  const int ntaps = __popc(mask);
+  if (tid == 0) {
+    int k = 0;
+    for (uint32_t m = mask; m; m &= m - 1) sTaps[k++] = __ffs(m) - 1;
+  }
+  __syncthreads();
+
+  const int cpt = (Ci + KC - 1) / KC;  // chunks per tap, the last one zero-padded
+  const int nchunks = ntaps * cpt;
+  f32x16_t acc;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+
+  P ra[AL], rb[BL];
+  P zero;
+  __builtin_memset(&zero, 0, sizeof(P));
+  auto load_chunk = [&](int c) {
+    const int ti = c / cpt;
+    const int ci0 = (c - ti * cpt) * KC;
+    const int v = sTaps[ti];
+#pragma unroll
+    for (int j = 0; j < AL; ++j) {
+      const int q = tid + j * NT;
+      P val = zero;
+      if (q < BM * LPR) {
+        const int r = q / LPR, ci = ci0 + (q % LPR) * EPL;
+        const int32_t src = sNbr[r * kTaps + v];
+        if (src >= 0 && ci < Ci) val = *(const P*)(feats + (int64_t)src * Ci + ci);
+      }
+      ra[j] = val;
+    }
+#pragma unroll
+    for (int j = 0; j < BL; ++j) {
+      const int q = tid + j * NT;
+      P val = zero;
+      if (q < BN * LPR) {
+        const int r = q / LPR, ci = ci0 + (q % LPR) * EPL;
+        if (n0 + r < Co && ci < Ci)
+          val = *(const P*)(weight + ((int64_t)(n0 + r) * kTaps + v) * Ci + ci);
+      }
+      rb[j] = val;
+    }
+  };
+  // Piece k of row r sits at byte k*LW of the row's 32 bytes; its 16-byte half is swizzled.
+  auto lds_off = [](int r, int k) {
+    const int byte = k * LW;
+    return r * KB + swz<2>(r, byte >> 4) * 16 + (byte & 15);
+  };
+  auto store_chunk = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < AL; ++j) {
+      const int q = tid + j * NT;
+      if (q < BM * LPR) *(P*)(&sA[buf][lds_off(q / LPR, q % LPR)]) = ra[j];
+    }
+#pragma unroll
+    for (int j = 0; j < BL; ++j) {
+      const int q = tid + j * NT;
+      if (q < BN * LPR) *(P*)(&sB[buf][lds_off(q / LPR, q % LPR)]) = rb[j];
+    }
+  };
+
+  if (nchunks > 0) {
+    load_chunk(0);
+    store_chunk(0);
+  }
+  const int part = lane >> 5;
+  const int ar = wm * 32 + (lane & 31), br = wn * 32 + (lane & 31);
+  for (int c = 0; c < nchunks; ++c) {
+    const int buf = c & 1;
+    __syncthreads();
+    if (c + 1 < nchunks) load_chunk(c + 1);
+    const uint4 a = *(const uint4*)(&sA[buf][ar * KB + swz<2>(ar, part) * 16]);
+    const uint4 b = *(const uint4*)(&sB[buf][br * KB + swz<2>(br, part) * 16]);
+    mfma_piece<T>(a, b, acc);
+    if (c + 1 < nchunks) store_chunk(buf ^ 1);
+  }
+
+  const int co = n0 + wn * 32 + (lane & 31);
+  if (co >= Co) return;
+  const float bv = bias ? to_f32<T>(bias[co]) : 0.f;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int rl = wm * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+    const int32_t row = sRow[rl];
+    if (row < 0) continue;
+    const int64_t o = (int64_t)row * Co + co;
+    float val = acc[e] + bv;
+    if (EPI == TSC_EPI_BIAS_RESIDUAL) val += to_f32<T>(residual[o]);
+    out[o] = from_f32<T>(val);
+  }
+}
+
+template <typename T, int LW, int EPI>
+int launch_generic(tsc_ctx* ctx, const ConvArgs& a) {
+  const int32_t m_tiles = (int32_t)((a.N + kGenBM - 1) / kGenBM);
+  const int32_t n_tiles = (a.Co + kGenBN - 1) / kGenBN;
+  const int32_t per_xcd = tile_grid_per_xcd(m_tiles, n_tiles);
+  static const std::string name = std::string("conv_generic_kernel<") +
+      (sizeof(T) == 4 ? "f32" : std::is_same<T, __bf16>::value ? "bf16" : "f16") + ",p" +
+      std::to_string(LW) + (EPI == TSC_EPI_BIAS_RESIDUAL ? ",res>" : ">");
+  ProfScope p(ctx, name.c_str());
+  conv_generic_kernel<T, LW, EPI><<<(unsigned)per_xcd * 8u, kGenThreads, 0, ctx->stream>>>(
+      (const T*)a.feats, (const T*)a.weight, (const T*)a.bias, a.nbr, a.order, a.N, a.Ci, a.Co,
+      m_tiles, n_tiles, per_xcd, (const T*)a.residual, (T*)a.out);
+  return check_hip(hipGetLastError(), "conv launch");
+}
+
+template <typename T, int EPI>
+int dispatch_generic(tsc_ctx* ctx, const ConvArgs& a) {
+  // Widest piece that divides the row and the feats / weight addresses.
+  const uintptr_t al = (uintptr_t)a.feats | (uintptr_t)a.weight;
+  const int row = a.Ci * (int)sizeof(T);
+  auto fits = [&](int w) { return row % w == 0 && al % w == 0; };
+  if (fits(16)) return launch_generic<T, 16, EPI>(ctx, a);
+  if (fits(8)) return launch_generic<T, 8, EPI>(ctx, a);
+  if (sizeof(T) == 4 || fits(4)) return launch_generic<T, 4, EPI>(ctx, a);
+  if constexpr (sizeof(T) == 2) return launch_generic<T, 2, EPI>(ctx, a);
+  return fail(TSC_ERR_INVALID, "conv: misaligned feats / weight");
 }
 
 // Largest chunk (bytes per row) that divides the Ci row and is a multiple of 32 bytes.
@@ -1081,16 +1264,29 @@ int dispatch_tiles(tsc_ctx* ctx, const ConvArgs& a) {
 }
 
 template <typename T>
-int dispatch_epi(tsc_ctx* ctx, const ConvArgs& a) {
-  if (a.epilogue == TSC_EPI_BIAS_RESIDUAL) return dispatch_tiles<T, TSC_EPI_BIAS_RESIDUAL>(ctx, a);
-  return dispatch_tiles<T, TSC_EPI_BIAS>(ctx, a);
+int dispatch_epi(tsc_ctx* ctx, const ConvArgs& a, bool tuned) {
+  if (a.epilogue == TSC_EPI_BIAS_RESIDUAL)
+    return tuned ? dispatch_tiles<T, TSC_EPI_BIAS_RESIDUAL>(ctx, a)
+                 : dispatch_generic<T, TSC_EPI_BIAS_RESIDUAL>(ctx, a);
+  return tuned ? dispatch_tiles<T, TSC_EPI_BIAS>(ctx, a) : dispatch_generic<T, TSC_EPI_BIAS>(ctx, a);
 }
 
 }  // namespace
 
+// Shapes and buffers the tuned kernels take: rows of a multiple of 32 bytes, Co a multiple of 32
+// (whole MFMA column blocks), every buffer 16-byte aligned (16-byte row loads and stores).
+bool conv_tuned_shape(const ConvArgs& a) {
+  const int es = a.dtype == TSC_F32 ? 4 : 2;
+  auto al16 = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
+  return (a.Ci * es) % 32 == 0 && a.Co % 32 == 0 && al16(a.feats) && al16(a.weight) &&
+         al16(a.out) && (!a.bias || al16(a.bias)) &&
+         (a.epilogue != TSC_EPI_BIAS_RESIDUAL || al16(a.residual));
+}
+
 int conv_launch(tsc_ctx* ctx, const ConvArgs& a) {
   if (a.N == 0) return TSC_OK;
-  if (conv_gather_supported(a)) return conv_gather_launch(ctx, a);
+  const bool tuned = conv_tuned_shape(a);
+  if (tuned && conv_gather_supported(a)) return conv_gather_launch(ctx, a);
   if (a.plan && !a.order) {  // other shapes: the plan's Morton row order
     ConvArgs b = a;
     b.order = (const int32_t*)((const char*)a.plan + plan_layout(a.N).rows);
@@ -1098,9 +1294,9 @@ int conv_launch(tsc_ctx* ctx, const ConvArgs& a) {
     return conv_launch(ctx, b);
   }
   switch (a.dtype) {
-    case TSC_F32: return dispatch_epi<float>(ctx, a);
-    case TSC_F16: return dispatch_epi<_Float16>(ctx, a);
-    case TSC_BF16: return dispatch_epi<__bf16>(ctx, a);
+    case TSC_F32: return dispatch_epi<float>(ctx, a, tuned);
+    case TSC_F16: return dispatch_epi<_Float16>(ctx, a, tuned);
+    case TSC_BF16: return dispatch_epi<__bf16>(ctx, a, tuned);
   }
   return fail(TSC_ERR_INVALID, "conv: unknown dtype %d", a.dtype);
 }

@@ -86,9 +86,11 @@ __global__ void morton_kernel(const int32_t* __restrict__ coords, int64_t N, int
 }
 
 // One wave per 64-row tile: distinct neighbor rows, their slots, the slot table and tap masks.
+// sorted_rows and rows_out may be the same buffer (the launcher sorts in place): each lane reads
+// its own entry before writing it, so neither is declared __restrict__.
 __global__ void __launch_bounds__(64 * kPlanWaves)
-    plan_tile_kernel(const int32_t* __restrict__ sorted_rows, const int32_t* __restrict__ nbr,
-                     int64_t N, int64_t T, int32_t* __restrict__ rows_out,
+    plan_tile_kernel(const int32_t* sorted_rows, const int32_t* __restrict__ nbr,
+                     int64_t N, int64_t T, int32_t* rows_out,
                      int32_t* __restrict__ count_out, uint32_t* __restrict__ rbm_out,
                      int32_t* __restrict__ list_out, uint4* __restrict__ slots_out) {
   __shared__ __attribute__((aligned(16))) int32_t hkey[kPlanWaves][kHash];
@@ -505,9 +507,9 @@ int launch_gather(tsc_ctx* ctx, const ConvArgs& a) {
   const int32_t n_tiles = (int32_t)L.T;
   const int32_t tpx = (n_tiles + 7) / 8;
   const int32_t halves = a.Co / 32;
-  static const std::string name = std::string("conv_gather_") +
+  static const std::string name = std::string("conv_gather_kernel<") +
       (std::is_same<T, __bf16>::value ? "bf16" : "f16") +
-      (EPI == TSC_EPI_BIAS_RESIDUAL ? "_res" : "");
+      (EPI == TSC_EPI_BIAS_RESIDUAL ? ",res>" : ">");
   ProfScope ps(ctx, name.c_str());
   conv_gather_kernel<T, EPI><<<256, 64 * kGWaves, 0, ctx->stream>>>(
       (const T*)a.feats, (const T*)a.weight, (const T*)a.bias, a.nbr,

@@ -118,6 +118,8 @@ struct ConvArgs {
   const void* plan = nullptr;  // gather plan (conv_gather.hip) or null
 };
 int conv_launch(tsc_ctx* ctx, const ConvArgs& a);
+// True when the tuned kernels take this shape and these buffers (else the generic kernel runs).
+bool conv_tuned_shape(const ConvArgs& a);
 
 // ---- gather plan + planned narrow conv (conv_gather.hip) ----
 constexpr int kPlanRows = 64;                   // rows per plan tile

@@ -125,6 +125,67 @@ def traffic(fetch_db: str, write_db: str, out_json: str, out_txt: str, calib_byt
     open(out_txt, "w").write("\n".join(lines) + "\n")
 
 
+def _durations(db: str) -> dict:
+    """{short kernel name: [duration us per dispatch]} from a kernel-trace database."""
+    agg = defaultdict(list)
+    for name, dur in _rows(db, "select name, duration from kernels"):
+        agg[short_name(name)].append(dur / 1e3)
+    return agg
+
+
+# MI355X: 256 CUs x 4 SIMDs; one MOPS unit of SQ_INSTS_VALU_MFMA_MOPS_* is 512 flops.
+SIMDS = 1024
+MOPS_FLOPS = 512
+
+
+def counters(pmc_db: str, trace_db: str, out_json: str, out_txt: str, command: str) -> None:
+    """Per-kernel averages of every counter in a --pmc database, with the MFMA figures derived
+    from them and the kernel durations of a --kernel-trace run of the same program:
+      mfma_tflops_hw  (sum of SQ_INSTS_VALU_MFMA_MOPS_*) * 512 / average duration: the flops the
+                      matrix cores executed, zero-padded work included
+      mfma_busy       SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE * 1024 SIMDs): the fraction of
+                      SIMD cycles with the MFMA unit busy while the GPU was active (rocprofv3's
+                      MfmaUtil expression)."""
+    names = [r[0] for r in _rows(pmc_db, "select distinct counter_name from counters_collection")]
+    per = {c: _counter(pmc_db, c) for c in names}
+    durs = _durations(trace_db) if trace_db else {}
+    res = {}
+    kernels = sorted({k for c in per.values() for k in c})
+    for name in kernels:
+        if "copyBuffer" in name or "fillBuffer" in name or "at::native" in name:
+            continue
+        key = short_name(name)
+        rec = {}
+        for c in names:
+            vals = [v for v, _ in per[c].get(name, [])]
+            if vals:
+                rec[c] = sum(vals) / len(vals)
+        if not rec:
+            continue
+        d = durs.get(key)
+        if d:
+            rec["avg_us"] = sum(d) / len(d)
+        mops = sum(rec.get(c, 0.0) for c in rec if c.startswith("SQ_INSTS_VALU_MFMA_MOPS_"))
+        if mops and rec.get("avg_us"):
+            rec["mfma_tflops_hw"] = mops * MOPS_FLOPS / (rec["avg_us"] * 1e-6) / 1e12
+        if rec.get("SQ_VALU_MFMA_BUSY_CYCLES") is not None and rec.get("GRBM_GUI_ACTIVE"):
+            rec["mfma_busy"] = rec["SQ_VALU_MFMA_BUSY_CYCLES"] / (rec["GRBM_GUI_ACTIVE"] * SIMDS)
+        res[key] = rec
+    doc = {"kernels": res, "command": command,
+           "formulas": {"mfma_tflops_hw": "sum(SQ_INSTS_VALU_MFMA_MOPS_*) * 512 / avg duration",
+                        "mfma_busy": "SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE * 1024 SIMDs)"}}
+    open(out_json, "w").write(json.dumps(doc, indent=1) + "\n")
+    lines = ["# rocprofv3 --pmc counters, average per dispatch",
+             f"# command: {command}",
+             "# mfma_tflops_hw = sum(SQ_INSTS_VALU_MFMA_MOPS_*) * 512 / avg duration (kernel trace);",
+             "# mfma_busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE * 1024 SIMDs)", ""]
+    for k, v in res.items():
+        lines.append(k)
+        for c, x in v.items():
+            lines.append(f"    {c:36s} {x:16.4f}" if isinstance(x, float) else f"    {c:36s} {x}")
+    open(out_txt, "w").write("\n".join(lines) + "\n")
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -132,6 +193,12 @@ def main() -> None:
     s.add_argument("db")
     s.add_argument("out")
     s.add_argument("--command", default="")
+    c = sub.add_parser("counters")
+    c.add_argument("pmc_db")
+    c.add_argument("trace_db")
+    c.add_argument("out_json")
+    c.add_argument("out_txt")
+    c.add_argument("--command", default="")
     t = sub.add_parser("traffic")
     t.add_argument("fetch_db")
     t.add_argument("write_db")
@@ -142,6 +209,8 @@ def main() -> None:
     a = ap.parse_args()
     if a.cmd == "stats":
         stats(a.db, a.out, a.command)
+    elif a.cmd == "counters":
+        counters(a.pmc_db, a.trace_db, a.out_json, a.out_txt, a.command)
     else:
         traffic(a.fetch_db, a.write_db, a.out_json, a.out_txt, a.calib_bytes, a.command)
 
