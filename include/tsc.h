@@ -156,6 +156,21 @@ int tsc_conv_fused(tsc_ctx* ctx, int32_t dtype, const void* feats, const void* w
                    int32_t Ci, int32_t Co, int32_t epilogue, const void* residual,
                    const void* ln_gamma, const void* ln_beta, float eps, void* out);
 
+/* tsc_conv_fused that allocates nothing: no hipMalloc / hipFree / allocating library call, for
+ * callers that cannot allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid device allocation).  Same arguments, kernels and results (bit for bit) as
+ * tsc_conv_fused; the only scratch it needs, the longest-first tile schedule of the 256-row
+ * tiles, lives in a static 512 KiB device array per GPU (held until the process ends) instead
+ * of the context's growable workspace.  N must not exceed 16777216 rows (65536 tiles of 256;
+ * TSC_ERR_INVALID beyond).  Every call on one GPU shares that array: calls that overlap on one
+ * device (different streams or contexts) race on it; calls on one stream are ordered.
+ * Per-kernel profiling (tsc_profile_enable) is suspended during the call.
+ * No counterpart in the reference (which allocates freely, conv3d.ts:144-221). */
+int tsc_conv_fused_noalloc(tsc_ctx* ctx, int32_t dtype, const void* feats, const void* weight,
+                           const void* bias, const int32_t* nbr, const int32_t* order, int64_t N,
+                           int32_t Ci, int32_t Co, int32_t epilogue, const void* residual,
+                           const void* ln_gamma, const void* ln_beta, float eps, void* out);
+
 /* tsc_conv_fused with a gather plan (tsc_map_gather_plan of the same coordinate set and map)
  * in place of the row order.  Ci = 32 with Co = 32 or 64 in fp16/bf16 runs the planned
  * kernel; other shapes run the tsc_conv_fused kernels in the plan's row order.  Same results

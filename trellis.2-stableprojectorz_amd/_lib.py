@@ -68,6 +68,8 @@ _SIGNATURES = {
     "tsc_conv": (_I32, [_P, _I32, _P, _P, _P, _P, _P, _I64, _I32, _I32, _P]),
     "tsc_conv_fused": (_I32, [_P, _I32, _P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _P, _P, _P,
                               _F32, _P]),
+    "tsc_conv_fused_noalloc": (_I32, [_P, _I32, _P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _P, _P,
+                                      _P, _F32, _P]),
     "tsc_layernorm": (_I32, [_P, _I32, _P, _I64, _I32, _P, _P, _F32, _I32, _P]),
     "tsc_silu": (_I32, [_P, _I32, _P, _I64, _P]),
     "tsc_add": (_I32, [_P, _I32, _P, _P, _I64, _P]),

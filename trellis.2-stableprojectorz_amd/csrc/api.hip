@@ -158,8 +158,13 @@ int tsc_ctx_create(int device, void* stream, tsc_ctx** out) {
   if (device < 0 || device >= ndev)
     return fail(TSC_ERR_INVALID, "ctx_create: device %d not in [0,%d)", device, ndev);
   DeviceGuard g(device);
+  // The device's static schedule scratch (tsc_conv_fused_noalloc), looked up while it is current.
+  void* scratch_dev = nullptr;
+  st = sched_scratch_ptr(device, &scratch_dev);
+  if (st) return st;
   tsc_ctx* c = new tsc_ctx();
   c->device = device;
+  c->sched_scratch = scratch_dev;
   c->ws = nullptr;
   c->ws_bytes = 0;
   c->stream = (hipStream_t)stream;  // NULL = the HIP null stream
@@ -403,6 +408,38 @@ int tsc_conv_fused(tsc_ctx* ctx, int32_t dtype, const void* feats, const void* w
   st = conv_launch(ctx, a);
   if (st || epilogue != TSC_EPI_BIAS_LN_SILU) return st;
   return layernorm_launch(ctx, dtype, out, N, Co, ln_gamma, ln_beta, eps, 1, out);
+}
+
+int tsc_conv_fused_noalloc(tsc_ctx* ctx, int32_t dtype, const void* feats, const void* weight,
+                           const void* bias, const int32_t* nbr, const int32_t* order, int64_t N,
+                           int32_t Ci, int32_t Co, int32_t epilogue, const void* residual,
+                           const void* ln_gamma, const void* ln_beta, float eps, void* out) {
+  g_err[0] = 0;
+  int st = validate_conv(ctx, dtype, feats, weight, bias, nbr, N, Ci, Co, out);
+  if (st) return st;
+  if (epilogue < TSC_EPI_BIAS || epilogue > TSC_EPI_BIAS_LN_SILU)
+    return fail(TSC_ERR_INVALID, "conv: unknown epilogue %d", epilogue);
+  if (epilogue == TSC_EPI_BIAS_RESIDUAL && N > 0 && (st = validate_residual(dtype, residual)))
+    return st;
+  if (N > kNoallocMaxRows)
+    return fail(TSC_ERR_INVALID, "conv_noalloc: N=%lld exceeds the static scratch limit of %lld "
+                                 "rows", (long long)N, (long long)kNoallocMaxRows);
+  if (N == 0) return TSC_OK;
+  if (!ctx->sched_scratch) return fail(TSC_ERR_HIP, "conv_noalloc: no scratch for this device");
+  DeviceGuard g(ctx->device);
+  // Per-kernel profiling records events (an allocation): off for this call.
+  const bool prof = ctx->profile;
+  ctx->profile = false;
+  ConvArgs a{dtype, feats, weight, bias, nbr, order, N, Ci, Co,
+             epilogue == TSC_EPI_BIAS_RESIDUAL ? TSC_EPI_BIAS_RESIDUAL : TSC_EPI_BIAS,
+             residual, out};
+  a.sched_scratch = ctx->sched_scratch;
+  a.sched_scratch_bytes = kSchedScratchBytes;
+  st = conv_launch(ctx, a);
+  if (!st && epilogue == TSC_EPI_BIAS_LN_SILU)
+    st = layernorm_launch(ctx, dtype, out, N, Co, ln_gamma, ln_beta, eps, 1, out);
+  ctx->profile = prof;
+  return st;
 }
 
 int tsc_layernorm(tsc_ctx* ctx, int32_t dtype, const void* x, int64_t N, int32_t C,

@@ -24,12 +24,44 @@
 // valid as long as A and B use the same one; here half h of micro-step s reads 16-byte LDS
 // piece 2s+h of the row.
 
+#include <mutex>
 #include <string>
 #include <type_traits>
+#include <vector>
 
 #include "tsc_internal.h"
 
 namespace tsc {
+
+// Schedule scratch of tsc_conv_fused_noalloc: one copy per device, alive until the process ends,
+// shared by every call on that device (calls that overlap on one device race on it).  Host code
+// must not pass `scratch` itself to a kernel: its host-side name is not the device address.  The
+// device address comes from hipGetSymbolAddress, once per device (sched_scratch_ptr).
+static __device__ __align__(256) int32_t scratch[kSchedScratchBytes / 4];
+
+int sched_scratch_ptr(int device, void** out) {
+  static std::mutex mu;
+  static std::vector<void*> ptrs;
+  std::lock_guard<std::mutex> lock(mu);
+  if (device < 0) return fail(TSC_ERR_INVALID, "scratch: bad device %d", device);
+  if ((size_t)device < ptrs.size() && ptrs[device]) {
+    *out = ptrs[device];
+    return TSC_OK;
+  }
+  int cur = -1;
+  int st = check_hip(hipGetDevice(&cur), "scratch: hipGetDevice");
+  if (st) return st;
+  if (cur != device) return fail(TSC_ERR_INVALID, "scratch: device %d is not current", device);
+  void* p = nullptr;
+  st = check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "scratch: hipGetSymbolAddress");
+  if (st) return st;
+  if (!p) return fail(TSC_ERR_HIP, "scratch: null symbol address");
+  if ((size_t)device >= ptrs.size()) ptrs.resize((size_t)device + 1, nullptr);
+  ptrs[device] = p;
+  *out = p;
+  return TSC_OK;
+}
+
 namespace {
 
 typedef __bf16 bf16x8_t __attribute__((__vector_size__(8 * sizeof(__bf16))));
@@ -177,7 +209,7 @@ constexpr int kTaps = 27;
 // and starts with its longest tiles.  Slots past the tile count get -1.  The schedule only
 // decides which block computes which tile: every tile's arithmetic is unchanged.
 constexpr int kSchedThreads = 256;
-constexpr int kSchedMaxTiles = 1 << 16;
+static_assert(kSchedMaxTiles == (1 << 16), "schedule bound shared with the scratch size");
 
 __global__ void __launch_bounds__(kSchedThreads)
     tile_cost_kernel(const int32_t* __restrict__ nbr, const int32_t* __restrict__ order, int64_t N,
@@ -716,9 +748,17 @@ int launch_cfg(tsc_ctx* ctx, const ConvArgs& a) {
   const int32_t* tile_map = nullptr;
   if (BM == 256 && m_tiles <= kSchedMaxTiles) {
     const int32_t lists = 8, per_list = (m_tiles + lists - 1) / lists;
+    const size_t need = ((size_t)m_tiles + (size_t)lists * per_list) * 4;
     void* ws;
-    int st = sched_workspace(ctx, ((size_t)m_tiles + (size_t)lists * per_list) * 4, &ws);
-    if (st) return st;
+    if (a.sched_scratch) {  // the caller's fixed buffer (tsc_conv_fused_noalloc)
+      if (need > a.sched_scratch_bytes)
+        return fail(TSC_ERR_INVALID, "conv: schedule needs %zu bytes of scratch, %zu available",
+                    need, a.sched_scratch_bytes);
+      ws = a.sched_scratch;
+    } else {
+      int st = sched_workspace(ctx, need, &ws);
+      if (st) return st;
+    }
     int32_t* cost = (int32_t*)ws;
     int32_t* map = cost + m_tiles;
     {

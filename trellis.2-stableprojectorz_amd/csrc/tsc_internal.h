@@ -41,6 +41,8 @@ struct tsc_ctx {
   hipEvent_t st_ev[2] = {nullptr, nullptr};
   bool st_pending[2] = {false, false};
   int st_next = 0;  // chunk the next load starts with
+  // Device address of this device's static schedule scratch (tsc_conv_fused_noalloc).
+  void* sched_scratch = nullptr;
   bool profile = false;
   std::vector<tsc_prof_rec> prof;      // pending launches
   std::vector<tsc_prof_agg> prof_agg;  // aggregated by tsc_profile_collect
@@ -116,7 +118,20 @@ struct ConvArgs {
   const void* residual;  // for TSC_EPI_BIAS_RESIDUAL
   void* out;
   const void* plan = nullptr;  // gather plan (conv_gather.hip) or null
+  // Device buffer for the 256-row tile schedule instead of the context's growable workspace
+  // (tsc_conv_fused_noalloc), and its size in bytes.
+  void* sched_scratch = nullptr;
+  size_t sched_scratch_bytes = 0;
 };
+// Row tiles the longest-first schedule handles (beyond it tiles run in row order), and the
+// schedule's largest scratch: a cost per tile plus 8 lists of ceil(tiles / 8) slots.
+constexpr int kSchedMaxTiles = 1 << 16;
+constexpr size_t kSchedScratchBytes = (size_t)2 * kSchedMaxTiles * 4;
+// Rows a tsc_conv_fused_noalloc call may have: every 256-row tile fits the schedule.
+constexpr int64_t kNoallocMaxRows = (int64_t)kSchedMaxTiles * 256;
+// The static schedule scratch of this device (conv.hip), found once per device by
+// hipGetSymbolAddress with that device current; null with an error status on failure.
+int sched_scratch_ptr(int device, void** out);
 int conv_launch(tsc_ctx* ctx, const ConvArgs& a);
 // True when the tuned kernels take this shape and these buffers (else the generic kernel runs).
 bool conv_tuned_shape(const ConvArgs& a);
