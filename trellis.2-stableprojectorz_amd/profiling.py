@@ -2,6 +2,10 @@
 
   python trellis.2-stableprojectorz_amd/profiling.py stats TRACE.db OUT.txt --command "..."
       per-kernel dispatch count, average / min / max duration and share of GPU time
+  python trellis.2-stableprojectorz_amd/profiling.py counters PMC.db TRACE.db OUT.json OUT.txt \
+          --command "..."
+      per-kernel averages of every --pmc counter, with MFMA throughput / busy fraction / clock
+      derived from them and the durations of a kernel-trace run of the same program
   python trellis.2-stableprojectorz_amd/profiling.py traffic FETCH.db WRITE.db OUT.json OUT.txt \
           --calib-bytes 268435456 --command "..."
       per-kernel average FETCH_SIZE and WRITE_SIZE (KiB per dispatch) scaled to bytes by the
@@ -133,8 +137,10 @@ def _durations(db: str) -> dict:
     return agg
 
 
-# MI355X: 256 CUs x 4 SIMDs; one MOPS unit of SQ_INSTS_VALU_MFMA_MOPS_* is 512 flops.
+# MI355X: 8 XCDs of 32 CUs x 4 SIMDs; one MOPS unit of SQ_INSTS_VALU_MFMA_MOPS_* is 512 flops.
+# rocprofv3 reports GRBM_GUI_ACTIVE per dispatch summed over the 8 XCD instances.
 SIMDS = 1024
+XCDS = 8
 MOPS_FLOPS = 512
 
 
@@ -143,9 +149,11 @@ def counters(pmc_db: str, trace_db: str, out_json: str, out_txt: str, command: s
     from them and the kernel durations of a --kernel-trace run of the same program:
       mfma_tflops_hw  (sum of SQ_INSTS_VALU_MFMA_MOPS_*) * 512 / average duration: the flops the
                       matrix cores executed, zero-padded work included
-      mfma_busy       SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE * 1024 SIMDs): the fraction of
-                      SIMD cycles with the MFMA unit busy while the GPU was active (rocprofv3's
-                      MfmaUtil expression)."""
+      mfma_busy       SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 * 1024 SIMDs): the fraction
+                      of SIMD cycles with the MFMA unit busy while the GPU was active (rocprofv3's
+                      MfmaUtil expression, which takes GRBM_GUI_ACTIVE of one XCD)
+      clock_ghz       GRBM_GUI_ACTIVE / 8 / average duration: the engine clock the kernel ran at
+                      (meaningful for kernels much longer than the counter set-up window)."""
     names = [r[0] for r in _rows(pmc_db, "select distinct counter_name from counters_collection")]
     per = {c: _counter(pmc_db, c) for c in names}
     durs = _durations(trace_db) if trace_db else {}
@@ -169,16 +177,22 @@ def counters(pmc_db: str, trace_db: str, out_json: str, out_txt: str, command: s
         if mops and rec.get("avg_us"):
             rec["mfma_tflops_hw"] = mops * MOPS_FLOPS / (rec["avg_us"] * 1e-6) / 1e12
         if rec.get("SQ_VALU_MFMA_BUSY_CYCLES") is not None and rec.get("GRBM_GUI_ACTIVE"):
-            rec["mfma_busy"] = rec["SQ_VALU_MFMA_BUSY_CYCLES"] / (rec["GRBM_GUI_ACTIVE"] * SIMDS)
+            xcd_cycles = rec["GRBM_GUI_ACTIVE"] / XCDS
+            rec["mfma_busy"] = rec["SQ_VALU_MFMA_BUSY_CYCLES"] / (xcd_cycles * SIMDS)
+            if rec.get("avg_us"):
+                rec["clock_ghz"] = xcd_cycles / (rec["avg_us"] * 1e3)
         res[key] = rec
     doc = {"kernels": res, "command": command,
            "formulas": {"mfma_tflops_hw": "sum(SQ_INSTS_VALU_MFMA_MOPS_*) * 512 / avg duration",
-                        "mfma_busy": "SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE * 1024 SIMDs)"}}
+                        "mfma_busy": "SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 * 1024 SIMDs)",
+                        "clock_ghz": "GRBM_GUI_ACTIVE / 8 / avg duration"}}
     open(out_json, "w").write(json.dumps(doc, indent=1) + "\n")
     lines = ["# rocprofv3 --pmc counters, average per dispatch",
              f"# command: {command}",
              "# mfma_tflops_hw = sum(SQ_INSTS_VALU_MFMA_MOPS_*) * 512 / avg duration (kernel trace);",
-             "# mfma_busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE * 1024 SIMDs)", ""]
+             "# mfma_busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 XCDs * 1024 SIMDs);",
+             "# clock_ghz = GRBM_GUI_ACTIVE / 8 / avg duration (GRBM_GUI_ACTIVE is summed over the",
+             "# 8 XCDs; short kernels include the counter set-up window)", ""]
     for k, v in res.items():
         lines.append(k)
         for c, x in v.items():
