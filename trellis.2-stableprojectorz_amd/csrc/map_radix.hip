@@ -566,75 +566,110 @@ struct ColumnLookup {
   }
 };
 
-// Window fill: a block owns kWinVox consecutive sorted voxels.  Their columns span
+// Window fill: a block owns VOX = ROUNDS * 28 consecutive sorted voxels (112).  Their columns span
 // [c_first, c_last]; every neighbor column with offset (kd-1)*dD along x lies in
 // [c_first + (kd-1)*dD*Y - dH, c_last + (kd-1)*dD*Y + dH], and the sorted voxels of those
-// columns are one contiguous run of the sorted arrays.  Phase 1 decodes the block's voxels once
-// (column, z, row, a 9-bit mask of in-grid neighbor columns, the duplicate check) and copies,
-// per kd, that run's rows and keys relative to the window's first column (j*Z + z for the j-th
-// column of the window; keys are unique, so a relative key names one voxel) plus the column
-// starts into LDS with coalesced loads; sentinel keys above every real one pad the run.
-// Phase 2 resolves every probe from LDS with 9 lanes per voxel (one per neighbor column, as in
-// the column-parallel fill): a binary search for the first key >= the lowest wanted one in the
-// column, then at most 2*dW + 1 consecutive entries, compared as keys (an entry of another
-// column or a sentinel cannot equal a wanted key).  A kd window that does not fit (very sparse or
-// very dense regions, or Z so large that window keys overflow 31 bits) falls back to the global
-// column lookup for that kd only.
+// columns are one contiguous run of the sorted arrays.  Phase 1 decodes the block's voxels (two
+// per thread, all loads issued together: column, z, row, a 9-bit mask of in-grid neighbor
+// columns, the duplicate check), then copies, per kd, that run's rows and keys relative to the
+// window's first column (j*Z + z for the j-th column of the window; keys are unique, so a
+// relative key names one voxel) plus the column starts into LDS, and takes the longest column
+// of the three windows from the same column-start loads.  Phase 2 resolves every probe from
+// LDS with 9 lanes per voxel (one per neighbor column): a binary search for the first key >= the
+// lowest wanted one in the column, then the next three entries compared as keys (an entry of
+// another column or a sentinel cannot equal a wanted key).  Each lane runs ILP voxels' searches
+// side by side, so ILP independent LDS chains are in flight per lane.  Blocks of a few hundred
+// voxels would amortise phase 1's chain of dependent global loads (own keys -> column starts ->
+// windows, several microseconds per block under the fill's write traffic) but measured slower
+// (fewer blocks per CU keep fewer scattered stores in flight); 112 voxels is the default.  A kd
+// window that does not fit (very sparse or very dense regions, or Z so large that window keys
+// overflow 31 bits) falls back to the global column lookup for that kd only.
 constexpr int kWinThreads = 256;
-constexpr int kWinRounds = 4;
-constexpr int kWinVox = kWinRounds * mapk::kFillVoxPerWave * (kWinThreads / 64);  // 112
-constexpr int kWinCapE = 464;  // voxels per kd window
-constexpr int kWinCapC = 432;  // columns per kd window (LDS < 20 KB per block: 8 blocks per CU)
+constexpr int kWinWaves = kWinThreads / 64;
+constexpr int kWinVoxPerRound = mapk::kFillVoxPerWave * kWinWaves;  // 28
+constexpr int kWinIlp = 4;
 
-template <typename K>
+template <int ROUNDS>
+struct WinCfg {
+  static constexpr int VOX = ROUNDS * kWinVoxPerRound;
+  // voxels / columns per kd window (LDS: 8 blocks per CU at 4 rounds, 4 at 16)
+  static constexpr int CAPE = ROUNDS >= 16 ? 1024 : ROUNDS >= 8 ? 640 : 464;
+  static constexpr int CAPC = ROUNDS >= 16 ? 256 : ROUNDS >= 8 ? 128 : 432;
+  static_assert(VOX <= 2 * kWinThreads, "two voxels per thread in the decode");
+  static_assert(ROUNDS % kWinIlp == 0, "rounds come in groups of ILP");
+};
+
+template <typename K, int ROUNDS>
 __global__ void __launch_bounds__(kWinThreads)
     fill_window_kernel(const K* __restrict__ keys, const int32_t* __restrict__ perm,
                        const int32_t* __restrict__ col_start, int64_t n, mapk::KeyCoder<K> kc_,
                        int32_t dD, int32_t dH, int32_t dW, int64_t ncol, int32_t per_xcd,
                        int32_t* __restrict__ nbr, uint32_t* __restrict__ status) {
+  using Cfg = WinCfg<ROUNDS>;
+  constexpr int VOX = Cfg::VOX, CAPE = Cfg::CAPE, CAPC = Cfg::CAPC;
   using I = typename std::conditional<sizeof(K) == 4, int32_t, int64_t>::type;  // column index
   // Window keys / rows at [1, ne], slot 0 readable (never used), sentinels after the run: the
   // probe reads up to 2 past a column's end and its search one before the column's start.
-  __shared__ int32_t lk[3][kWinCapE + 5];
-  __shared__ int32_t lp[3][kWinCapE + 5];
-  __shared__ int32_t lcs[3][kWinCapC + 1];
+  __shared__ int32_t lk[3][CAPE + 5];
+  __shared__ int32_t lp[3][CAPE + 5];
+  __shared__ int32_t lcs[3][CAPC + 1];
   __shared__ I w_lo[3];
   __shared__ int32_t w_e0[3], w_ne[3], w_nc[3];
   __shared__ I c_range[2];
   __shared__ int32_t w_maxlen;  // longest column in the three windows
-  __shared__ I vcol[kWinVox];
-  __shared__ int32_t vz[kWinVox], vrow[kWinVox], vmask[kWinVox];
+  __shared__ I vcol[VOX];       // absolute column (the global-lookup path)
+  __shared__ int4 vinfo[VOX];   // column - c_first, z, row, in-grid neighbor-column mask
   const int tid = threadIdx.x;
   const int32_t X = kc_.X, Y = kc_.Y, Z = kc_.Z;
   const int64_t logical = (int64_t)(blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
-  const int64_t i0 = logical * kWinVox;
+  const int64_t i0 = logical * VOX;
   if (i0 >= n) return;  // uniform per block
-  const int nv = (int)((i0 + kWinVox < n) ? kWinVox : n - i0);
-  int dup = 0;
-  for (int j = tid; j < nv; j += kWinThreads) {
-    const K key = keys[i0 + j];
-    K column;
+  const int nv = (int)((i0 + VOX < n) ? VOX : n - i0);
+  // Every thread decodes the block's first key (one broadcast load) for relative columns.
+  K first_col;
+  {
     int32_t x, y, z;
-    kc_.decode(key, &column, &x, &y, &z);
-    int m = 0;
-#pragma unroll
-    for (int kd = 0; kd < 3; ++kd) {
-#pragma unroll
-      for (int kh = 0; kh < 3; ++kh) {
-        const bool in = (uint32_t)(x + (kd - 1) * dD) < (uint32_t)X &&
-                        (uint32_t)(y + (kh - 1) * dH) < (uint32_t)Y;
-        m |= (int)in << (kd * 3 + kh);
-      }
-    }
-    vcol[j] = (I)column;
-    vz[j] = z;
-    vmask[j] = m;
-    vrow[j] = perm[i0 + j];
-    if (i0 + j > 0 && keys[i0 + j - 1] == key) dup = 1;
-    if (j == 0) c_range[0] = (I)column;
-    if (j == nv - 1) c_range[1] = (I)column;
+    kc_.decode(keys[i0], &first_col, &x, &y, &z);
   }
-  if (tid == 0) w_maxlen = 0;
+  int dup = 0;
+  {
+    K kk[2], kp[2];
+    int32_t rr[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int j = tid + h * kWinThreads;
+      const bool live = j < nv;
+      kk[h] = live ? keys[i0 + j] : (K)0;
+      kp[h] = (live && i0 + j > 0) ? keys[i0 + j - 1] : (K)-1;
+      rr[h] = live ? perm[i0 + j] : -1;
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int j = tid + h * kWinThreads;
+      if (j >= nv) continue;
+      K column;
+      int32_t x, y, z;
+      kc_.decode(kk[h], &column, &x, &y, &z);
+      int m = 0;
+#pragma unroll
+      for (int kd = 0; kd < 3; ++kd) {
+#pragma unroll
+        for (int kh = 0; kh < 3; ++kh) {
+          const bool in = (uint32_t)(x + (kd - 1) * dD) < (uint32_t)X &&
+                          (uint32_t)(y + (kh - 1) * dH) < (uint32_t)Y;
+          m |= (int)in << (kd * 3 + kh);
+        }
+      }
+      vcol[j] = (I)column;
+      vinfo[j] = make_int4((int32_t)(column - first_col), z, rr[h], m);
+      if (kp[h] == kk[h]) dup = 1;
+      if (j == nv - 1) c_range[1] = (I)column;
+    }
+  }
+  if (tid == 0) {
+    c_range[0] = (I)first_col;
+    w_maxlen = 0;
+  }
   dup = __syncthreads_or(dup);
   if (dup && tid == 0) atomicOr(status, TSC_MAP_DUPLICATE);
   if (tid < 3) {
@@ -644,12 +679,15 @@ __global__ void __launch_bounds__(kWinThreads)
     if (hi > ncol - 1) hi = ncol - 1;
     int32_t e0 = 0, ne = 0, nc = 0;
     // Window keys (j*Z + z) must stay below 2^31 - 1 (the sentinel).
-    const bool keys31 = (int64_t)(kWinCapC + 1) * Z < (int64_t)INT32_MAX;
-    if (lo <= hi && hi - lo + 1 <= kWinCapC && keys31) {
+    const bool keys31 = (int64_t)(CAPC + 1) * Z < (int64_t)INT32_MAX;
+    if (lo <= hi && hi - lo + 1 <= CAPC && keys31) {
       e0 = col_start[lo];
       ne = col_start[hi + 1] - e0;
       nc = (int32_t)(hi - lo + 1);
-      if (ne > kWinCapE) nc = -1;
+      if (ne > CAPE) {
+        nc = -1;
+        ne = 0;  // nothing copied (the sentinels then sit at the window's start)
+      }
     } else if (lo <= hi) {
       nc = -1;
     }
@@ -659,36 +697,60 @@ __global__ void __launch_bounds__(kWinThreads)
     w_nc[tid] = nc;  // -1: window does not fit, probes of this kd go to global memory
   }
   __syncthreads();
-#pragma unroll
-  for (int w = 0; w < 3; ++w) {
-    const int nc = w_nc[w];
-    if (nc <= 0) continue;
-    const I lo = w_lo[w];
-    const int32_t e0 = w_e0[w], ne = w_ne[w];
-    const K kbase = (K)lo * (K)Z;  // key of the window's first column at z = 0
-    for (int j = tid; j <= nc; j += kWinThreads) lcs[w][j] = col_start[lo + j] - e0;
-    for (int j = tid; j < ne; j += kWinThreads) {
-      lk[w][1 + j] = (int32_t)(keys[e0 + j] - kbase);
-      lp[w][1 + j] = perm[e0 + j];
-    }
-    if (tid < 4) lk[w][1 + ne + tid] = INT32_MAX;
-  }
-  __syncthreads();
-
   {
+    // Column starts (and the longest column), then keys and rows of the three windows: the loads
+    // of each group are issued before its LDS stores.
     int mx = 0;
 #pragma unroll
     for (int w = 0; w < 3; ++w) {
       const int nc = w_nc[w];
-      for (int j = tid; j < nc; j += kWinThreads) mx = max(mx, lcs[w][j + 1] - lcs[w][j]);
+      if (nc <= 0) continue;  // empty (lo > hi) or not fitting: no column starts
+      const I lo = w_lo[w];
+      const int32_t e0 = w_e0[w];
+      for (int j = tid; j <= nc; j += kWinThreads) {
+        const int32_t a = col_start[lo + j];
+        const int32_t b = j < nc ? col_start[lo + j + 1] : a;
+        lcs[w][j] = a - e0;
+        mx = max(mx, b - a);
+      }
     }
-    if (mx > 0) atomicMax(&w_maxlen, mx);
+#pragma unroll
+    for (int w = 0; w < 3; ++w) {
+      const int nc = w_nc[w];
+      if (nc <= 0) continue;
+      const int32_t e0 = w_e0[w], ne = w_ne[w];
+      const K kbase = (K)w_lo[w] * (K)Z;  // key of the window's first column at z = 0
+      for (int j0 = 0; j0 < ne; j0 += 4 * kWinThreads) {
+        K kv[4];
+        int32_t pv[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int j = j0 + u * kWinThreads + tid;
+          kv[u] = j < ne ? keys[e0 + j] : (K)0;
+          pv[u] = j < ne ? perm[e0 + j] : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int j = j0 + u * kWinThreads + tid;
+          if (j < ne) {
+            lk[w][1 + j] = (int32_t)(kv[u] - kbase);
+            lp[w][1 + j] = pv[u];
+          }
+        }
+      }
+    }
+    // Sentinels after every window's run, also for empty and global-lookup windows (whose lanes
+    // still read entries 0..2 and must find no key they want).
+    if (tid < 12) lk[tid >> 2][1 + w_ne[tid >> 2] + (tid & 3)] = INT32_MAX;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = max(mx, __shfl_xor(mx, off, 64));
+    if ((tid & 63) == 0 && mx > 0) atomicMax(&w_maxlen, mx);
   }
   __syncthreads();
 
   const int lane = tid & 63, wid = tid >> 6;
   const int slot = lane / mapk::kFillLanes, col = lane - slot * mapk::kFillLanes;
-  if (slot >= mapk::kFillVoxPerWave) return;
+  if (slot >= mapk::kFillVoxPerWave) return;  // no barrier follows
   const int kd = col / 3, kh = col - kd * 3;
   const int nc_w = w_nc[kd];
   const I lo_w = w_lo[kd];
@@ -696,66 +758,79 @@ __global__ void __launch_bounds__(kWinThreads)
   const int32_t* const wk = lk[kd] + 1;
   const int32_t* const wp = lp[kd] + 1;
   const int32_t* const wc = lcs[kd];
-  const int li0 = wid * kWinRounds * mapk::kFillVoxPerWave + slot;
+  const int li0 = wid * ROUNDS * mapk::kFillVoxPerWave + slot;
   if (dW == 1 && w_nc[0] >= 0 && w_nc[1] >= 0 && w_nc[2] >= 0) {
     // Every window fits (block-uniform): branch-free probes.  The neighbor column is window
-    // column j (an in-grid neighbor column always lies in the window) and the wanted keys are
-    // t - 1, t, t + 1 with t = j*Z + z.  The first entry >= t - 1 comes from a binary search
-    // over the column with a block-uniform step count (powers of two below the longest column);
-    // the three keys can only be that entry and the next two.  Out-of-grid lanes search an empty
-    // range and want negative keys, which match nothing.
+    // column j = (column - c_first) + jofs (an in-grid neighbor column always lies in the
+    // window) and the wanted keys are t - 1, t, t + 1 with t = j*Z + z.  The first entry >= t - 1
+    // comes from a binary search over the column with a block-uniform step count (powers of two
+    // below the longest column); the three keys can only be that entry and the next two.
+    // Out-of-grid lanes search an empty range and want negative keys, which match nothing.
+    const int jofs = (int)((I)c_range[0] + off - lo_w);
+    const int maxlen = w_maxlen;
     int steps = 0;
-    while ((2 << steps) <= w_maxlen) ++steps;  // 2^steps <= maxlen < 2^(steps+1)
-    const int top = w_maxlen > 0 ? 1 << steps : 0;
+    while ((2 << steps) <= maxlen) ++steps;  // 2^steps <= maxlen < 2^(steps+1)
+    const int top = maxlen > 0 ? 1 << steps : 0;
+    for (int g = 0; g < ROUNDS; g += kWinIlp) {
+      int pos[kWinIlp], e[kWinIlp], first[kWinIlp], t[kWinIlp], zz[kWinIlp], row[kWinIlp];
+      bool live[kWinIlp];
 #pragma unroll
-    for (int r = 0; r < kWinRounds; ++r) {
-      const int li = li0 + r * mapk::kFillVoxPerWave;
-      const bool live = li < nv;
-      const int lic = live ? li : 0;
-      const int32_t row = vrow[lic];
-      const int32_t z = vz[lic];
-      const bool inb = ((vmask[lic] >> col) & 1) && live;
-      const int j = inb ? (int)(vcol[lic] + off - lo_w) : 0;
-      const int a = inb ? wc[j] : 0;
-      const int e = inb ? wc[j + 1] : 0;
-      const int32_t t = inb ? j * Z + z : -4;
-      const int32_t first = z > 0 ? t - 1 : t;
-      int pos = a;
-      for (int st = top; st > 0; st >>= 1) {  // uniform trip count, no lane branches
-        const int tt = pos + st;
-        const int32_t kv = wk[(tt < e ? tt : e) - 1];  // index >= a - 1 >= -1
-        pos = ((tt <= e) & (kv < first)) ? tt : pos;
+      for (int u = 0; u < kWinIlp; ++u) {
+        const int li = li0 + (g + u) * mapk::kFillVoxPerWave;
+        live[u] = li < nv;
+        const int4 vi = vinfo[live[u] ? li : 0];
+        row[u] = vi.z;
+        zz[u] = vi.y;
+        const bool inb = live[u] && ((vi.w >> col) & 1);
+        const int j = inb ? vi.x + jofs : 0;
+        pos[u] = inb ? wc[j] : 0;
+        e[u] = inb ? wc[j + 1] : 0;
+        t[u] = inb ? j * Z + zz[u] : -4;
+        first[u] = zz[u] > 0 ? t[u] - 1 : t[u];
       }
-      // pos <= e <= ne: pos + 2 reads a later column's key or a sentinel at worst.
-      const int32_t k0 = wk[pos], k1 = wk[pos + 1], k2 = wk[pos + 2];
-      const int32_t p0 = wp[pos], p1 = wp[pos + 1], p2 = wp[pos + 2];
-      const int32_t tm = z > 0 ? t - 1 : -4, tp = z + 1 < Z ? t + 1 : -4;
-      const int32_t v0 = k0 == tm ? p0 : -1;
-      int32_t v1 = k1 == t ? p1 : -1;
-      v1 = k0 == t ? p0 : v1;
-      int32_t v2 = k2 == tp ? p2 : -1;
-      v2 = k1 == tp ? p1 : v2;
-      v2 = k0 == tp ? p0 : v2;
-      if (col == 4) v1 = row;  // tap 13 is the voxel itself
-      if (live) {
-        int32_t* dst = nbr + (int64_t)row * 27 + col * 3;
-        dst[0] = v0;
-        dst[1] = v1;
-        dst[2] = v2;
+      for (int st = top; st > 0; st >>= 1) {  // uniform trip count, no lane branches
+#pragma unroll
+        for (int u = 0; u < kWinIlp; ++u) {
+          const int tt = pos[u] + st;
+          const int32_t kv = wk[(tt < e[u] ? tt : e[u]) - 1];  // index >= a - 1 >= -1
+          pos[u] = ((tt <= e[u]) & (kv < first[u])) ? tt : pos[u];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kWinIlp; ++u) {
+        // pos <= e <= ne: pos + 2 reads a later column's key or a sentinel at worst.
+        const int p = pos[u];
+        const int32_t k0 = wk[p], k1 = wk[p + 1], k2 = wk[p + 2];
+        const int32_t p0 = wp[p], p1 = wp[p + 1], p2 = wp[p + 2];
+        const int32_t tm = zz[u] > 0 ? t[u] - 1 : -4, tp = zz[u] + 1 < Z ? t[u] + 1 : -4;
+        const int32_t v0 = k0 == tm ? p0 : -1;
+        int32_t v1 = k1 == t[u] ? p1 : -1;
+        v1 = k0 == t[u] ? p0 : v1;
+        int32_t v2 = k2 == tp ? p2 : -1;
+        v2 = k1 == tp ? p1 : v2;
+        v2 = k0 == tp ? p0 : v2;
+        if (col == 4) v1 = row[u];  // tap 13 is the voxel itself
+        if (live[u]) {
+          int32_t* dst = nbr + (int64_t)row[u] * 27 + col * 3;
+          dst[0] = v0;
+          dst[1] = v1;
+          dst[2] = v2;
+        }
       }
     }
     return;
   }
   const int nscan = 2 * dW + 1;
   ColumnLookup<K, true> glk{keys, col_start, perm, n};
-  for (int r = 0; r < kWinRounds; ++r) {
+  for (int r = 0; r < ROUNDS; ++r) {
     const int li = li0 + r * mapk::kFillVoxPerWave;
     if (li >= nv) break;
-    const int32_t row = vrow[li];
+    const int4 vi = vinfo[li];
+    const int32_t row = vi.z;
     int32_t v0 = -1, v1 = -1, v2 = -1;
-    if ((vmask[li] >> col) & 1) {
+    if ((vi.w >> col) & 1) {
       const I ncl = vcol[li] + off;
-      const int32_t z = vz[li];
+      const int32_t z = vi.y;
       const bool has_lo = z - dW >= 0, has_hi = z + dW < Z;
       if (nc_w > 0) {
         const int j = (int)(ncl - lo_w);
@@ -770,7 +845,7 @@ __global__ void __launch_bounds__(kWinThreads)
           else b = mid;
         }
         const int32_t last = base + (has_hi ? z + dW : z);
-        for (int t = 0; t < nscan; ++t, ++a) {
+        for (int s = 0; s < nscan; ++s, ++a) {
           if (a >= e) break;
           const int32_t kk = wk[a];
           if (kk > last) break;
@@ -804,6 +879,10 @@ inline int bit_length(uint64_t v) {
   }
   return b;
 }
+
+// Rounds per fill block: 4 (112 voxels, 8 blocks per CU).  Measured on map512: 8 rounds (224
+// voxels, 7 blocks per CU) +6 % and 16 rounds (448 voxels, 4 blocks per CU) +22 % fill time.
+constexpr int kFillRounds = 4;
 
 template <typename K>
 int radix_impl(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t B, int32_t X, int32_t Y,
@@ -870,9 +949,10 @@ int radix_impl(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t B, int32_
     ProfScope ps(ctx, "radix_fill");
     const K no_sentinel = (K)-1;  // out-of-range voxels were clamped in pack
     if (use_cols) {
-      const int64_t blocks = (N + kWinVox - 1) / kWinVox;
+      constexpr int R = kFillRounds;
+      const int64_t blocks = (N + WinCfg<R>::VOX - 1) / WinCfg<R>::VOX;
       const int32_t per_xcd = (int32_t)((blocks + 7) / 8);
-      fill_window_kernel<K><<<(unsigned)per_xcd * 8u, kWinThreads, 0, s>>>(
+      fill_window_kernel<K, R><<<(unsigned)per_xcd * 8u, kWinThreads, 0, s>>>(
           kOut, vOut, cols, N, mapk::KeyCoder<K>::make(X, Y, Z), dil[0], dil[1], dil[2], ncol,
           per_xcd, nbr_out, status_dev);
     } else {
