@@ -2,8 +2,9 @@
 
 Usage: python build.py [--jobs N]
 
-Every .hip file under csrc/ is compiled with hipcc for gfx950 and linked into one shared
-library exporting the C ABI declared in include/tsc.h.  Object files go to _build/ (ignored by
+Every .hip file under csrc/ is compiled with hipcc for gfx950 (and every .cpp file, host-only
+C++, with the same compiler) and linked into one shared library exporting the C ABI declared in
+include/tsc.h.  Object files go to _build/ (ignored by
 git); the .so lands in this package directory so that it travels with the source tree.
 """
 from __future__ import annotations
@@ -50,7 +51,7 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     if not Path(HIPCC).exists() and shutil.which("hipcc") is None:
         raise RuntimeError("hipcc not found; cannot build libtrellis_sparse.so")
     BUILD.mkdir(exist_ok=True)
-    sources = sorted(CSRC.glob("*.hip"))
+    sources = sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
     jobs = jobs or min(len(sources), os.cpu_count() or 1, 8)
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(_compile, sources))

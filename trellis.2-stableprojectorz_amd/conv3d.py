@@ -28,13 +28,15 @@ def neighbor_cache_key(kernel_size, dilation) -> str:
 
 
 def get_neighbor_map(x: SparseTensor, kernel_size=(3, 3, 3), dilation=(1, 1, 1),
-                     method: str = "auto") -> ops.NeighborMap:
-    """The cached neighbor map of x's voxels, built on first use."""
+                     method: str = "auto", validate: bool = False) -> ops.NeighborMap:
+    """The cached neighbor map of x's voxels, built on first use.  The build is only enqueued
+    (the status word is not read back unless validate=True; NeighborMap.check() reads it), so with
+    x's spatial shape and batch size known on the host the conv path never synchronizes."""
     key = neighbor_cache_key(kernel_size, dilation)
     nmap = x.get_spatial_cache(key)
     if nmap is None:
         nmap = ops.build_neighbor_map(x.coords, x.spatial_shape, x.batch_size, dilation,
-                                      kernel_size, method)
+                                      kernel_size, method, validate=validate)
         x.register_spatial_cache(key, nmap)
     return nmap
 

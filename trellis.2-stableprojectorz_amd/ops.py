@@ -54,8 +54,15 @@ class NeighborMap:
     batch_size: int
     dilation: tuple
     coords: torch.Tensor | None = None  # the (N,4) input, kept for the gather plan
+    status: torch.Tensor | None = None  # device int32 (1): TSC_MAP_* bits, 0 = valid
     _conv_order: torch.Tensor | None = None
     _gather_plan: torch.Tensor | None = None
+
+    def check(self) -> None:
+        """Reads the build's status word (one 4-byte device-to-host copy, which waits for the
+        build) and raises on duplicate or out-of-range coordinates, whose outputs are undefined."""
+        if self.status is not None:
+            _raise_status(int(self.status.item()), self.batch_size, self.spatial_shape)
 
     def conv_order(self) -> torch.Tensor:
         """Row order the convs use (tsc_map_conv_order), computed on first use and cached."""
@@ -107,13 +114,26 @@ def map_gather_plan(coords: torch.Tensor, nbr: torch.Tensor, batch_size: int,
     return plan
 
 
+def _raise_status(st: int, batch_size, spatial_shape) -> None:
+    if st:
+        X, Y, Z = spatial_shape
+        what = []
+        if st & _lib.TSC_MAP_DUPLICATE:
+            what.append("duplicate coordinates")
+        if st & _lib.TSC_MAP_OUT_OF_RANGE:
+            what.append(f"coordinates outside [0,{batch_size})x[0,{X})x[0,{Y})x[0,{Z})")
+        raise TscError(_lib.TSC_ERR_INVALID, "map build: " + ", ".join(what))
+
+
 def build_neighbor_map(coords: torch.Tensor, spatial_shape, batch_size: int,
                        dilation=(1, 1, 1), kernel_size=(3, 3, 3), method: str = "auto",
                        validate: bool = True) -> NeighborMap:
     """Neighbor map of int32 (N,4) [b,x,y,z] coords on the GPU.
 
     validate=True reads the device status word back (one 4-byte sync) and raises on duplicate or
-    out-of-range coordinates, whose outputs are undefined.
+    out-of-range coordinates, whose outputs are undefined.  validate=False only enqueues the
+    build (the operator path: the reference never checks either); NeighborMap.check() reads the
+    status later.
     """
     if coords.dtype != torch.int32 or coords.dim() != 2 or coords.shape[1] != 4:
         raise TscError(_lib.TSC_ERR_INVALID, "coords must be int32 of shape (N,4)")
@@ -133,16 +153,11 @@ def build_neighbor_map(coords: torch.Tensor, spatial_shape, batch_size: int,
     d = (ctypes.c_int32 * 3)(*dilation)
     check(ctx.lib.tsc_map_build(ctx.bind(), _p(coords), n, int(batch_size), X, Y, Z, k, d,
                                 _lib.MAP_METHODS[method], _p(keys), _p(perm), _p(nbr), _p(status)))
+    nmap = NeighborMap(nbr, keys, perm, (X, Y, Z), int(batch_size), tuple(dilation), coords,
+                       status)
     if validate:
-        st = int(status.item())
-        if st:
-            what = []
-            if st & _lib.TSC_MAP_DUPLICATE:
-                what.append("duplicate coordinates")
-            if st & _lib.TSC_MAP_OUT_OF_RANGE:
-                what.append(f"coordinates outside [0,{batch_size})x[0,{X})x[0,{Y})x[0,{Z})")
-            raise TscError(_lib.TSC_ERR_INVALID, "map build: " + ", ".join(what))
-    return NeighborMap(nbr, keys, perm, (X, Y, Z), int(batch_size), tuple(dilation), coords)
+        nmap.check()
+    return nmap
 
 
 def _nbr_and_order(nmap, order):

@@ -54,8 +54,14 @@ def compute_layout(coords: torch.Tensor) -> list[tuple[int, int]]:
 
 
 class SparseTensor:
+    """spatial_shape / batch_size may be given by the caller (host ints, e.g. the model's grid
+    resolution): the conv path then never reads device values back, so SparseConv3d.forward only
+    enqueues work.  Otherwise they are computed from the coordinates on first use (one
+    device-to-host read each, cached), as are the per-batch row ranges (`layout`)."""
+
     def __init__(self, feats: torch.Tensor, coords: torch.Tensor, shape=None,
-                 scale: Scale | None = None, cache: dict | None = None, layout=None):
+                 scale: Scale | None = None, cache: dict | None = None, layout=None,
+                 spatial_shape=None, batch_size: int | None = None):
         if coords.dim() != 2 or coords.shape[1] != 4:
             raise ValueError("coords must be (N,4) [batch,x,y,z]")
         if feats.shape[0] != coords.shape[0]:
@@ -65,7 +71,10 @@ class SparseTensor:
         self._shape = list(shape) if shape is not None else None
         self._scale = scale or SCALE_IDENTITY
         self._spatial_cache = cache if cache is not None else {}
-        self.layout = layout if layout is not None else compute_layout(coords)
+        self._layout = layout
+        self._batch_size = int(batch_size) if batch_size is not None else None
+        if spatial_shape is not None:
+            self.register_spatial_cache("shape", [int(v) for v in spatial_shape])
 
     # ---- properties ---------------------------------------------------------------------
     @property
@@ -77,8 +86,17 @@ class SparseTensor:
         return self.feats.dtype
 
     @property
+    def layout(self) -> list[tuple[int, int]]:
+        """Per-batch (start, stop) row ranges, computed on first use (sparse_tensor.ts:216-237)."""
+        if self._layout is None:
+            self._layout = compute_layout(self.coords)
+        return self._layout
+
+    @property
     def batch_size(self) -> int:
-        return len(self.layout)
+        if self._batch_size is None:
+            self._batch_size = len(self.layout)
+        return self._batch_size
 
     @property
     def shape(self) -> list[int]:
@@ -117,12 +135,16 @@ class SparseTensor:
 
     # ---- replace (sparse_tensor.ts:112-121) ---------------------------------------------
     def replace(self, feats: torch.Tensor, coords: torch.Tensor | None = None) -> "SparseTensor":
+        """New feats (and optionally coords) with this tensor's shape, scale, spatial cache and
+        layout, as the reference's replace (sparse_tensor.ts:112-121)."""
         return SparseTensor(feats, self.coords if coords is None else coords, self._shape,
-                            self._scale, self._spatial_cache, self.layout)
+                            self._scale, self._spatial_cache, self._layout,
+                            batch_size=self._batch_size)
 
     def to(self, device) -> "SparseTensor":
         return SparseTensor(self.feats.to(device), self.coords.to(device), self._shape,
-                            self._scale, self._spatial_cache, self.layout)
+                            self._scale, self._spatial_cache, self._layout,
+                            batch_size=self._batch_size)
 
     @staticmethod
     def from_feats_and_coords(feats_list, coords_list) -> "SparseTensor":
