@@ -61,18 +61,35 @@ __global__ void __launch_bounds__(PT)
   __syncthreads();
   const int64_t base = (int64_t)blockIdx.x * PTILE;
   int oob = 0;
+  // All PI coordinate loads are issued before the first store, and full tiles run without
+  // per-item branches: one vmcnt counts loads and stores, and across branches the compiler
+  // falls back to waiting for everything, which would serialise the items on store latency.
+  int4 c[PI];
+  auto item = [&](int j, int64_t e) {
+    K key;
+    if (!mapk::pack_key<K>(c[j], B, X, Y, Z, &key)) {
+      key = last_cell;
+      oob = 1;
+    }
+    keys[e] = key;
+    vals[e] = (int32_t)e;
+    atomicAdd(&hist[digit_of<K>(key, shift, mask)], 1);  // LDS atomic
+  };
+  if (base + PTILE <= N) {
 #pragma unroll
-  for (int j = 0; j < PI; ++j) {
-    const int64_t e = base + j * PT + threadIdx.x;
-    if (e < N) {
-      K key;
-      if (!mapk::pack_key<K>(coords[e], B, X, Y, Z, &key)) {
-        key = last_cell;
-        oob = 1;
-      }
-      keys[e] = key;
-      vals[e] = (int32_t)e;
-      atomicAdd(&hist[digit_of<K>(key, shift, mask)], 1);  // LDS atomic
+    for (int j = 0; j < PI; ++j) c[j] = coords[base + j * PT + threadIdx.x];
+#pragma unroll
+    for (int j = 0; j < PI; ++j) item(j, base + j * PT + threadIdx.x);
+  } else {
+#pragma unroll
+    for (int j = 0; j < PI; ++j) {
+      const int64_t e = base + j * PT + threadIdx.x;
+      c[j] = e < N ? coords[e] : make_int4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < PI; ++j) {
+      const int64_t e = base + j * PT + threadIdx.x;
+      if (e < N) item(j, e);
     }
   }
   oob = __syncthreads_or(oob);
@@ -584,28 +601,28 @@ struct ColumnLookup {
 // (fewer blocks per CU keep fewer scattered stores in flight); 112 voxels is the default.  A kd
 // window that does not fit (very sparse or very dense regions, or Z so large that window keys
 // overflow 31 bits) falls back to the global column lookup for that kd only.
-constexpr int kWinThreads = 256;
-constexpr int kWinWaves = kWinThreads / 64;
-constexpr int kWinVoxPerRound = mapk::kFillVoxPerWave * kWinWaves;  // 28
 constexpr int kWinIlp = 4;
 
-template <int ROUNDS>
+// THREADS per block (2 or 4 waves), ROUNDS of 7 voxels per wave; CAPE / CAPC = voxels / columns
+// per kd window, sized so that the LDS lets the wave limit (32 per CU) decide the blocks per CU.
+template <int ROUNDS, int THREADS>
 struct WinCfg {
-  static constexpr int VOX = ROUNDS * kWinVoxPerRound;
-  // voxels / columns per kd window (LDS: 8 blocks per CU at 4 rounds, 4 at 16)
-  static constexpr int CAPE = ROUNDS >= 16 ? 1024 : ROUNDS >= 8 ? 640 : 464;
-  static constexpr int CAPC = ROUNDS >= 16 ? 256 : ROUNDS >= 8 ? 128 : 432;
-  static_assert(VOX <= 2 * kWinThreads, "two voxels per thread in the decode");
+  static constexpr int WAVES = THREADS / 64;
+  static constexpr int VOX = ROUNDS * mapk::kFillVoxPerWave * WAVES;
+  static constexpr int CAPE = THREADS == 128 ? 240 : ROUNDS >= 16 ? 1024 : ROUNDS >= 8 ? 640 : 464;
+  static constexpr int CAPC = THREADS == 128 ? 96 : ROUNDS >= 16 ? 256 : ROUNDS >= 8 ? 128 : 432;
+  static_assert(VOX <= 2 * THREADS, "two voxels per thread in the decode");
   static_assert(ROUNDS % kWinIlp == 0, "rounds come in groups of ILP");
 };
 
-template <typename K, int ROUNDS>
-__global__ void __launch_bounds__(kWinThreads)
+template <typename K, int ROUNDS, int THREADS>
+__global__ void __launch_bounds__(THREADS)
     fill_window_kernel(const K* __restrict__ keys, const int32_t* __restrict__ perm,
                        const int32_t* __restrict__ col_start, int64_t n, mapk::KeyCoder<K> kc_,
                        int32_t dD, int32_t dH, int32_t dW, int64_t ncol, int32_t per_xcd,
                        int32_t* __restrict__ nbr, uint32_t* __restrict__ status) {
-  using Cfg = WinCfg<ROUNDS>;
+  using Cfg = WinCfg<ROUNDS, THREADS>;
+  constexpr int kWinThreads = THREADS;
   constexpr int VOX = Cfg::VOX, CAPE = Cfg::CAPE, CAPC = Cfg::CAPC;
   using I = typename std::conditional<sizeof(K) == 4, int32_t, int64_t>::type;  // column index
   // Window keys / rows at [1, ne], slot 0 readable (never used), sentinels after the run: the
@@ -698,44 +715,55 @@ __global__ void __launch_bounds__(kWinThreads)
   }
   __syncthreads();
   {
-    // Column starts (and the longest column), then keys and rows of the three windows: the loads
-    // of each group are issued before its LDS stores.
+    // Column starts (and the longest column), keys and rows of the three windows: every load of
+    // this phase is issued before the first LDS store (one round trip instead of one per window
+    // and array).  Each thread takes column entries j = tid + 256u (u < CU) and window entries
+    // j = tid + 256u (u < EU) of every window; indices past a window's end are clamped to its last
+    // entry (or to entry 0 of an empty window) so that every load is unconditional.
+    constexpr int CU = (CAPC + 1 + kWinThreads - 1) / kWinThreads;
+    constexpr int EU = (CAPE + kWinThreads - 1) / kWinThreads;
+    int32_t ca[3][CU], cb[3][CU], pv[3][EU];
+    K kv[3][EU];
+#pragma unroll
+    for (int w = 0; w < 3; ++w) {
+      const int nc = w_nc[w] > 0 ? w_nc[w] : 0;
+      const int64_t lo = w_nc[w] > 0 ? (int64_t)w_lo[w] : 0;
+      const int ne = w_nc[w] > 0 ? w_ne[w] : 0;
+      const int64_t e0 = ne > 0 ? w_e0[w] : 0;
+#pragma unroll
+      for (int u = 0; u < CU; ++u) {
+        const int j = min(tid + u * kWinThreads, nc);
+        ca[w][u] = col_start[lo + j];
+        cb[w][u] = col_start[lo + min(j + 1, nc)];
+      }
+#pragma unroll
+      for (int u = 0; u < EU; ++u) {
+        const int j = min(tid + u * kWinThreads, ne > 0 ? ne - 1 : 0);
+        kv[w][u] = keys[e0 + j];
+        pv[w][u] = perm[e0 + j];
+      }
+    }
     int mx = 0;
 #pragma unroll
     for (int w = 0; w < 3; ++w) {
       const int nc = w_nc[w];
-      if (nc <= 0) continue;  // empty (lo > hi) or not fitting: no column starts
-      const I lo = w_lo[w];
-      const int32_t e0 = w_e0[w];
-      for (int j = tid; j <= nc; j += kWinThreads) {
-        const int32_t a = col_start[lo + j];
-        const int32_t b = j < nc ? col_start[lo + j + 1] : a;
-        lcs[w][j] = a - e0;
-        mx = max(mx, b - a);
-      }
-    }
-#pragma unroll
-    for (int w = 0; w < 3; ++w) {
-      const int nc = w_nc[w];
-      if (nc <= 0) continue;
+      if (nc <= 0) continue;  // empty (lo > hi) or not fitting: nothing copied
       const int32_t e0 = w_e0[w], ne = w_ne[w];
       const K kbase = (K)w_lo[w] * (K)Z;  // key of the window's first column at z = 0
-      for (int j0 = 0; j0 < ne; j0 += 4 * kWinThreads) {
-        K kv[4];
-        int32_t pv[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int j = j0 + u * kWinThreads + tid;
-          kv[u] = j < ne ? keys[e0 + j] : (K)0;
-          pv[u] = j < ne ? perm[e0 + j] : 0;
+      for (int u = 0; u < CU; ++u) {
+        const int j = tid + u * kWinThreads;
+        if (j <= nc) {
+          lcs[w][j] = ca[w][u] - e0;
+          mx = max(mx, cb[w][u] - ca[w][u]);
         }
+      }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int j = j0 + u * kWinThreads + tid;
-          if (j < ne) {
-            lk[w][1 + j] = (int32_t)(kv[u] - kbase);
-            lp[w][1 + j] = pv[u];
-          }
+      for (int u = 0; u < EU; ++u) {
+        const int j = tid + u * kWinThreads;
+        if (j < ne) {
+          lk[w][1 + j] = (int32_t)(kv[w][u] - kbase);
+          lp[w][1 + j] = pv[w][u];
         }
       }
     }
@@ -880,9 +908,12 @@ inline int bit_length(uint64_t v) {
   return b;
 }
 
-// Rounds per fill block: 4 (112 voxels, 8 blocks per CU).  Measured on map512: 8 rounds (224
-// voxels, 7 blocks per CU) +6 % and 16 rounds (448 voxels, 4 blocks per CU) +22 % fill time.
-constexpr int kFillRounds = 4;
+// Voxels per fill block: 112.  Measured on map512: 224 voxels (7 blocks per CU) +6 % and 448
+// voxels (4 blocks per CU) +22 % fill time.
+// Threads per fill block: 256 (4 waves, 8 blocks per CU).  2-wave blocks of the same 112 voxels
+// (16 blocks per CU, twice the dependent load chains in flight) measured 9 % slower.
+constexpr int kFillThreads = 256;
+constexpr int kFillRounds = 1024 / kFillThreads;  // 112 voxels per block
 
 template <typename K>
 int radix_impl(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t B, int32_t X, int32_t Y,
@@ -949,10 +980,10 @@ int radix_impl(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t B, int32_
     ProfScope ps(ctx, "radix_fill");
     const K no_sentinel = (K)-1;  // out-of-range voxels were clamped in pack
     if (use_cols) {
-      constexpr int R = kFillRounds;
-      const int64_t blocks = (N + WinCfg<R>::VOX - 1) / WinCfg<R>::VOX;
+      constexpr int R = kFillRounds, T = kFillThreads;
+      const int64_t blocks = (N + WinCfg<R, T>::VOX - 1) / WinCfg<R, T>::VOX;
       const int32_t per_xcd = (int32_t)((blocks + 7) / 8);
-      fill_window_kernel<K, R><<<(unsigned)per_xcd * 8u, kWinThreads, 0, s>>>(
+      fill_window_kernel<K, R, T><<<(unsigned)per_xcd * 8u, T, 0, s>>>(
           kOut, vOut, cols, N, mapk::KeyCoder<K>::make(X, Y, Z), dil[0], dil[1], dil[2], ncol,
           per_xcd, nbr_out, status_dev);
     } else {
