@@ -113,6 +113,18 @@ def test_plan_dense_blocks_and_ragged_tail(pkg, dev):
     assert (c2 < 0).any()
 
 
+def test_plan_large_morton_buckets(pkg, dev):
+    """A dense 32x64x8 block in 512^3 fills one 10-bit Morton prefix (a 32x64x64 cell region)
+    with 16384 voxels: four chunks of the bucket kernel's bitmap rank."""
+    g = np.stack(np.meshgrid(np.arange(32) + 32, np.arange(64) + 64, np.arange(8) + 128,
+                             indexing="ij"), -1).reshape(-1, 3)
+    xyz = np.concatenate([g, [[0, 0, 0], [511, 511, 511], [40, 100, 200]]])
+    coords = np.concatenate([np.zeros((len(xyz), 1), np.int64), xyz], 1).astype(np.int32)
+    coords = coords[np.random.default_rng(6).permutation(len(coords))]
+    print(f"  gather plan dense slab in 512^3 N={len(coords)}", flush=True)
+    _check_plan(pkg, dev, coords, 1, (512, 512, 512))
+
+
 def _pair(pkg, dev, coords, batch, shape, ci, co, dtype, epilogue, dil=(1, 1, 1), seed=0):
     m = pkg.build_neighbor_map(torch.from_numpy(coords).to(dev), shape, batch, dil)
     n = len(coords)

@@ -108,6 +108,18 @@ def test_map_dense_and_sparse_extremes(pkg, dev, method):
         _build(pkg, dev, dup, 1, (64, 64, 64), method=method)
 
 
+@pytest.mark.parametrize("method", METHODS)
+def test_map_bucket_over_65536(pkg, dev, method):
+    """A dense 256x512 half slice of 512^3 is one 2^17-cell key bucket of 131072 voxels: past the
+    bitmap rank's 16-bit prefixes, so the radix path sorts it by LSD passes."""
+    yz = np.stack(np.meshgrid(np.arange(256), np.arange(512), indexing="ij"), -1).reshape(-1, 2)
+    c = np.concatenate([np.zeros((len(yz), 1), np.int64), np.full((len(yz), 1), 7), yz], 1)
+    c = np.concatenate([c, [[0, 6, 3, 3], [0, 8, 255, 511], [0, 400, 1, 2]]]).astype(np.int32)
+    c = c[np.random.default_rng(8).permutation(len(c))]
+    m = _build(pkg, dev, c, 1, (512, 512, 512), method=method)
+    _check(m, c, 1, (512, 512, 512), (1, 1, 1))
+
+
 def test_map_empty(pkg, dev):
     c = torch.zeros((0, 4), dtype=torch.int32, device=dev)
     m = pkg.build_neighbor_map(c, (4, 4, 4), 1)

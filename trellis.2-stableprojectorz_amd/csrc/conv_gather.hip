@@ -23,8 +23,6 @@
 // order, so the 16 rows of one (tap, row block) mostly sit in consecutive slots (distinct LDS
 // banks for the fragment reads).
 
-#include <rocprim/device/device_radix_sort.hpp>
-
 #include <climits>
 #include <string>
 #include <type_traits>
@@ -63,27 +61,6 @@ constexpr int kHashShift = 23;     // 32 - log2(kHash)
 constexpr int kPrioWords = 56;     // 1792 priorities / 32
 constexpr int kPlanWaves = 4;
 constexpr int kTableQ = kPlanTableBytes / 16;  // 112 uint4 per tile table
-
-// Morton code of voxel i (Z-curve over x, y, z; z lowest), the batch index above it, reduced to
-// its top 64 bits when wider.  vals[i] = i.
-template <typename K>
-__global__ void morton_kernel(const int32_t* __restrict__ coords, int64_t N, int bits, int shift,
-                              K* __restrict__ keys, int32_t* __restrict__ vals) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= N) return;
-  const int4 c = ((const int4*)coords)[i];
-  uint64_t m = 0;
-  for (int b = 0; b < bits; ++b) {  // bits <= 21
-    m |= (uint64_t)((c.w >> b) & 1) << (3 * b);
-    m |= (uint64_t)((c.z >> b) & 1) << (3 * b + 1);
-    m |= (uint64_t)((c.y >> b) & 1) << (3 * b + 2);
-  }
-  // (batch, morton) as one key; `shift` drops low Morton bits when the pair exceeds 64 bits
-  const uint64_t key = shift > 0 ? ((uint64_t)c.x << (3 * bits - shift)) | (m >> shift)
-                                 : ((uint64_t)c.x << (3 * bits)) | m;
-  keys[i] = (K)key;  // K = uint32_t only when the key has at most 32 bits
-  vals[i] = (int32_t)i;
-}
 
 // One wave per 64-row tile: distinct neighbor rows, their slots, the slot table and tap masks.
 // sorted_rows and rows_out may be the same buffer (the launcher sorts in place): each lane reads
@@ -552,37 +529,11 @@ int gather_plan_launch(tsc_ctx* ctx, const int32_t* coords, const int32_t* nbr, 
   const int total = 3 * bits + bitlen((int64_t)B - 1);
   // Keys wider than 64 bits drop their lowest Morton bits: a coarser curve, still a permutation.
   const int shift = total > 64 ? total - 64 : 0;
-  const int end_bit = std::max(1, std::min(64, total));
+  const int nbits = std::max(1, std::min(64, total));
   char* base = (char*)plan;
   int32_t* rows = (int32_t*)(base + L.rows);
-  // Morton keys of up to 32 bits sort as uint32 (half the key traffic of the 64-bit sort).
-  auto sort = [&](auto key_tag) -> int {
-    using K = decltype(key_tag);
-    size_t temp_bytes = 0;
-    hipError_t e = rocprim::radix_sort_pairs(nullptr, temp_bytes, (K*)nullptr, (K*)nullptr,
-                                             (int32_t*)nullptr, (int32_t*)nullptr, (size_t)N, 0,
-                                             end_bit, ctx->stream);
-    if (e != hipSuccess) return check_hip(e, "gather plan sort size");
-    const size_t need = 2 * align_up((size_t)N * sizeof(K), 256) + align_up((size_t)N * 4, 256) +
-                        align_up(temp_bytes, 256);
-    void* ws;
-    int st = workspace(ctx, need, &ws);
-    if (st) return st;
-    Carve cv(ws);
-    K* kin = cv.take<K>(N);
-    K* kout = cv.take<K>(N);
-    int32_t* vin = cv.take<int32_t>(N);
-    void* temp = cv.take<char>(temp_bytes);
-    morton_kernel<K><<<(unsigned)((N + 255) / 256), 256, 0, ctx->stream>>>(coords, N, bits, shift,
-                                                                            kin, vin);
-    st = check_hip(hipGetLastError(), "gather plan keys");
-    if (st) return st;
-    e = rocprim::radix_sort_pairs(temp, temp_bytes, kin, kout, vin, rows, (size_t)N, 0, end_bit,
-                                  ctx->stream);
-    return e == hipSuccess ? TSC_OK : check_hip(e, "gather plan sort");
-  };
   ProfScope ps(ctx, "gather_plan");
-  const int st = end_bit <= 32 ? sort(uint32_t{}) : sort(uint64_t{});
+  const int st = sort_rows_morton(ctx, coords, N, bits, shift, nbits, rows);
   if (st) return st;
   const unsigned blocks = (unsigned)((L.T + kPlanWaves - 1) / kPlanWaves);
   plan_tile_kernel<<<blocks, 64 * kPlanWaves, 0, ctx->stream>>>(

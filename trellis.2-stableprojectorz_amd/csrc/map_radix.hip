@@ -17,6 +17,8 @@
 //              in the bucket's key range, by binary search of the sorted bucket in LDS.
 //   fill       window fill from LDS (below), or the column-parallel fill over the whole sorted
 //              array when the column table would be much larger than the voxel set.
+// The gather plan sorts its rows by Morton key with the same pack / scan / partition / bucket
+// stages (sort_rows_morton, no column starts).
 
 #include <algorithm>
 #include <type_traits>
@@ -38,7 +40,6 @@ constexpr int LPT = LNB / RT;       // local digits owned per thread
 constexpr int PT = 512;             // pack / partition threads per block
 constexpr int PI = 16;              // pack / partition items per thread
 constexpr int PTILE = PT * PI;      // pack / partition tile
-constexpr int PDPT = NBMAX / PT;    // bucket digits owned per thread in the partition prefix
 
 template <typename K>
 __device__ __forceinline__ int digit_of(K k, int shift, int mask) {
@@ -49,12 +50,52 @@ __global__ void clear_status_kernel(uint32_t* status) {
   if (threadIdx.x == 0) status[0] = 0u;
 }
 
+// Key generators for pack_kernel.  PackedKey: the (b, x, y, z) cell index of the neighbor map,
+// clamped to the last cell (and reported) when out of range.  MortonKey: the gather plan's
+// (batch, Z-curve) key over the low `bits` bits of x, y, z (z lowest), its lowest `shift` bits
+// dropped when the pair is wider than 64 bits, masked to the sort's key width.
 template <typename K>
+struct PackedKey {
+  int32_t B, X, Y, Z;
+  K last_cell;
+  __device__ __forceinline__ bool operator()(int4 c, K* key) const {
+    if (mapk::pack_key<K>(c, B, X, Y, Z, key)) return true;
+    *key = last_cell;
+    return false;
+  }
+};
+
+// Spreads the low 21 bits of v to every third bit (bit i -> bit 3i), by the shift-and-mask
+// sequence of "bit interleaving by magic numbers" (each step halves the width of the groups).
+__device__ __forceinline__ uint64_t spread3(uint32_t v) {
+  uint64_t x = v & 0x1fffffu;
+  x = (x | x << 32) & 0x001f00000000ffffull;
+  x = (x | x << 16) & 0x001f0000ff0000ffull;
+  x = (x | x << 8) & 0x100f00f00f00f00full;
+  x = (x | x << 4) & 0x10c30c30c30c30c3ull;
+  x = (x | x << 2) & 0x1249249249249249ull;
+  return x;
+}
+
+template <typename K>
+struct MortonKey {
+  int bits, shift;
+  uint64_t mask;
+  __device__ __forceinline__ bool operator()(int4 c, K* key) const {
+    const uint32_t lo = (uint32_t)((1u << bits) - 1u);
+    const uint64_t m = spread3((uint32_t)c.w & lo) | spread3((uint32_t)c.z & lo) << 1 |
+                       spread3((uint32_t)c.y & lo) << 2;
+    const uint64_t k = ((uint64_t)(uint32_t)c.x << (3 * bits - shift)) | (m >> shift);
+    *key = (K)(k & mask);
+    return true;
+  }
+};
+
+template <typename K, typename Gen>
 __global__ void __launch_bounds__(PT)
-    pack_kernel(const int4* __restrict__ coords, int64_t N, int32_t B, int32_t X, int32_t Y,
-                int32_t Z, K last_cell, K* __restrict__ keys, int32_t* __restrict__ vals,
-                int shift, int dbits, int* __restrict__ counts, int ntiles,
-                int* __restrict__ oob_tile) {
+    pack_kernel(const int4* __restrict__ coords, int64_t N, Gen gen, K* __restrict__ keys,
+                int32_t* __restrict__ vals, int shift, int dbits, int* __restrict__ counts,
+                int ntiles, int* __restrict__ oob_tile) {
   __shared__ int hist[NBMAX];
   const int nb = 1 << dbits, mask = nb - 1;
   for (int d = threadIdx.x; d < nb; d += PT) hist[d] = 0;
@@ -67,10 +108,7 @@ __global__ void __launch_bounds__(PT)
   int4 c[PI];
   auto item = [&](int j, int64_t e) {
     K key;
-    if (!mapk::pack_key<K>(c[j], B, X, Y, Z, &key)) {
-      key = last_cell;
-      oob = 1;
-    }
+    if (!gen(c[j], &key)) oob = 1;
     keys[e] = key;
     vals[e] = (int32_t)e;
     atomicAdd(&hist[digit_of<K>(key, shift, mask)], 1);  // LDS atomic
@@ -190,6 +228,7 @@ __global__ void __launch_bounds__(PT)
                      int shift, int dbits, const int* __restrict__ offs,
                      const int* __restrict__ totals, int ntiles, K* __restrict__ kdst,
                      int32_t* __restrict__ vdst, int* __restrict__ bstart) {
+  constexpr int PDPT = NBMAX / PT;  // bucket digits owned per thread in the prefix
   __shared__ int lcnt[NBMAX];
   __shared__ int dstart[NBMAX];
   __shared__ int gbase[NBMAX];
@@ -312,10 +351,11 @@ __device__ __forceinline__ void wave_offsets(int (*wcnt)[LNB], int (&cnt)[LPT]) 
 
 // One block per bucket b (see the file comment).  The bucket occupies [start, start+size) of
 // (k0, v0) after the partition.
-//  * size <= RTILE and lb <= kBitmapBits (every int32-key grid up to 2^27 cells): each thread
-//    loads its elements into registers and sets bit (key mod 2^lb) of an LDS bitmap of the
-//    bucket's key range.  With unique keys an element's sorted position is the number of set
-//    bits below its own (per-word prefix counts + one popcount), and so is every column start:
+//  * size <= 65536 and lb <= kBitmapBits (every int32-key grid up to 2^27 cells): each thread
+//    sets bit (key mod 2^lb) of an LDS bitmap of the bucket's key range for its elements (held
+//    in registers up to RTILE elements, else read in chunks of RTILE).  With unique keys an
+//    element's sorted position is the number of set bits below its own (per-word prefix counts
+//    + one popcount), and so is every column start:
 //    col_start[c] = start + (set bits below c*Z - (b << lb)).
 //  * otherwise, or when the bitmap finds a repeated key: stable LSD passes over the bucket's
 //    remaining bits (at most 9 per pass) through global memory in chunks of RTILE (histogram of
@@ -338,7 +378,6 @@ __global__ void __launch_bounds__(RT)
   __shared__ __attribute__((aligned(16))) uint16_t wpre[kBitmapWords];  // set bits before each word
   __shared__ int wsum[WAVES];
   static_assert(kBitmapWords >= LNB * (WAVES + 1), "LSD counters alias the bitmap");
-  static_assert(RTILE <= 65535, "prefix counts fit 16 bits");
   uint32_t* bits = smem;
   int* run = (int*)smem;
   int(*wcnt)[LNB] = (int(*)[LNB])((int*)smem + LNB);
@@ -351,29 +390,51 @@ __global__ void __launch_bounds__(RT)
   const K lmask = (K)(((uint64_t)1 << lb) - 1);
 
   bool by_bitmap = false;
-  if (size <= RTILE && lb <= kBitmapBits && passes > 0) {
+  // 16-bit word prefixes hold ranks below 65536: larger buckets take the LSD path.
+  if (size <= 65536 && lb <= kBitmapBits && passes > 0) {
     const int nwords = ((1 << lb) + 31) / 32;
     for (int i = tid; i < nwords; i += RT) bits[i] = 0u;
     __syncthreads();
+    // A bucket of at most RTILE elements stays in registers; a larger one is read in chunks of
+    // RTILE twice (bits, then ranks) and written by rank straight to the outputs.
+    const bool in_regs = size <= RTILE;
     K kk[RI];
     int32_t vv[RI];
     int loc[RI];
     int dup = 0;
+    if (in_regs) {
 #pragma unroll
-    for (int j = 0; j < RI; ++j) {
-      const int i = j * RT + tid;
-      if (i < size) {
-        kk[j] = k0[start + i];
-        vv[j] = v0[start + i];
+      for (int j = 0; j < RI; ++j) {
+        const int i = j * RT + tid;
+        if (i < size) {
+          kk[j] = k0[start + i];
+          vv[j] = v0[start + i];
+        }
       }
-    }
 #pragma unroll
-    for (int j = 0; j < RI; ++j) {
-      const int i = j * RT + tid;
-      if (i < size) {
-        loc[j] = (int)(kk[j] & lmask);
-        const uint32_t bit = 1u << (loc[j] & 31);
-        dup |= (atomicOr(&bits[loc[j] >> 5], bit) & bit) != 0u;
+      for (int j = 0; j < RI; ++j) {
+        const int i = j * RT + tid;
+        if (i < size) {
+          loc[j] = (int)(kk[j] & lmask);
+          const uint32_t bit = 1u << (loc[j] & 31);
+          dup |= (atomicOr(&bits[loc[j] >> 5], bit) & bit) != 0u;
+        }
+      }
+    } else {
+      for (int c0 = 0; c0 < size; c0 += RTILE) {
+#pragma unroll
+        for (int j = 0; j < RI; ++j) {
+          const int i = c0 + j * RT + tid;
+          kk[j] = i < size ? k0[start + i] : (K)0;
+        }
+#pragma unroll
+        for (int j = 0; j < RI; ++j) {
+          if (c0 + j * RT + tid < size) {
+            const int l = (int)(kk[j] & lmask);
+            const uint32_t bit = 1u << (l & 31);
+            dup |= (atomicOr(&bits[l >> 5], bit) & bit) != 0u;
+          }
+        }
       }
     }
     dup = __syncthreads_or(dup);
@@ -430,50 +491,67 @@ __global__ void __launch_bounds__(RT)
         }
       }
       __syncthreads();
-      int rk[RI];
-#pragma unroll
-      for (int j = 0; j < RI; ++j) {
-        const int i = j * RT + tid;
-        if (i < size) {
-          const int wi = loc[j] >> 5;
-          rk[j] = wpre[wi] + __popc(bits[wi] & ((1u << (loc[j] & 31)) - 1u));
-        }
-      }
+      // Rank of local key l among the bucket's keys: set bits below it.
+      auto rank = [&](int l) {
+        const int wi = l >> 5;
+        return (int)wpre[wi] + __popc(bits[wi] & ((1u << (l & 31)) - 1u));
+      };
       // Column starts from the bitmap, before the staging below overwrites it: columns whose
       // first key c*Z lies in this bucket's key range [b << lb, (b+1) << lb).
       if (col_start) {
         const int64_t key_lo = (int64_t)b << lb;
         const int64_t key_hi = std::min<int64_t>((int64_t)(b + 1) << lb, cells);
         const int64_t c_lo = (key_lo + Z - 1) / Z, c_hi = (key_hi + Z - 1) / Z;
-        for (int64_t c = c_lo + tid; c < c_hi; c += RT) {
-          const int local = (int)(c * Z - key_lo);
-          const int wi = local >> 5;
-          col_start[c] = (int32_t)(start + wpre[wi] + __popc(bits[wi] & ((1u << (local & 31)) - 1u)));
-        }
+        for (int64_t c = c_lo + tid; c < c_hi; c += RT)
+          col_start[c] = (int32_t)(start + rank((int)(c * Z - key_lo)));
       }
-      if constexpr (sizeof(K) == 4) {
-        // Stage keys, then rows, in sorted order through LDS (the bitmap is no longer needed)
-        // so that the global writes are coalesced runs instead of one cache line per element.
-        int32_t* st = (int32_t*)smem;
-        static_assert(kBitmapWords >= RTILE, "staging holds a full bucket");
-        __syncthreads();
+      if (in_regs) {
+        int rk[RI];
 #pragma unroll
         for (int j = 0; j < RI; ++j)
-          if (j * RT + tid < size) st[rk[j]] = (int32_t)kk[j];
-        __syncthreads();
-        for (int i = tid; i < size; i += RT) kout[start + i] = (K)st[i];
-        __syncthreads();
+          if (j * RT + tid < size) rk[j] = rank(loc[j]);
+        if constexpr (sizeof(K) == 4) {
+          // Stage keys, then rows, in sorted order through LDS (the bitmap is no longer
+          // needed) so that the global writes are coalesced runs instead of one cache line per
+          // element.
+          int32_t* st = (int32_t*)smem;
+          static_assert(kBitmapWords >= RTILE, "staging holds a full bucket");
+          __syncthreads();
 #pragma unroll
-        for (int j = 0; j < RI; ++j)
-          if (j * RT + tid < size) st[rk[j]] = vv[j];
-        __syncthreads();
-        for (int i = tid; i < size; i += RT) vout[start + i] = st[i];
+          for (int j = 0; j < RI; ++j)
+            if (j * RT + tid < size) st[rk[j]] = (int32_t)kk[j];
+          __syncthreads();
+          for (int i = tid; i < size; i += RT) kout[start + i] = (K)st[i];
+          __syncthreads();
+#pragma unroll
+          for (int j = 0; j < RI; ++j)
+            if (j * RT + tid < size) st[rk[j]] = vv[j];
+          __syncthreads();
+          for (int i = tid; i < size; i += RT) vout[start + i] = st[i];
+        } else {
+#pragma unroll
+          for (int j = 0; j < RI; ++j) {
+            if (j * RT + tid < size) {
+              kout[start + rk[j]] = kk[j];
+              vout[start + rk[j]] = vv[j];
+            }
+          }
+        }
       } else {
+        for (int c0 = 0; c0 < size; c0 += RTILE) {
 #pragma unroll
-        for (int j = 0; j < RI; ++j) {
-          if (j * RT + tid < size) {
-            kout[start + rk[j]] = kk[j];
-            vout[start + rk[j]] = vv[j];
+          for (int j = 0; j < RI; ++j) {
+            const int i = c0 + j * RT + tid;
+            kk[j] = i < size ? k0[start + i] : (K)0;
+            vv[j] = i < size ? v0[start + i] : 0;
+          }
+#pragma unroll
+          for (int j = 0; j < RI; ++j) {
+            if (c0 + j * RT + tid < size) {
+              const int r = rank((int)(kk[j] & lmask));
+              kout[start + r] = kk[j];
+              vout[start + r] = vv[j];
+            }
           }
         }
       }
@@ -915,22 +993,77 @@ inline int bit_length(uint64_t v) {
 constexpr int kFillThreads = 256;
 constexpr int kFillRounds = 1024 / kFillThreads;  // 112 voxels per block
 
+// Sort buffers carved from one workspace: (kA, vA) and (kB, vB) ping-pong copies of the pairs,
+// per-(bucket, tile) counts, bucket totals and starts, per-tile out-of-range flags.
+template <typename K>
+struct SortBufs {
+  K *kA, *kB;
+  int32_t *vA, *vB;
+  int *counts, *totals, *oob_tile, *bstart;
+  static size_t bytes(int64_t N, int nb) {
+    const int64_t ntiles = (N + PTILE - 1) / PTILE;
+    return 2 * align_up((size_t)N * sizeof(K), 256) + 2 * align_up((size_t)N * 4, 256) +
+           align_up((size_t)nb * ntiles * 4, 256) + 2 * align_up((size_t)nb * 4, 256) +
+           align_up((size_t)ntiles * 4, 256);
+  }
+  void carve(Carve& cv, int64_t N, int nb) {
+    const int64_t ntiles = (N + PTILE - 1) / PTILE;
+    kA = cv.take<K>(N);
+    vA = cv.take<int32_t>(N);
+    kB = cv.take<K>(N);
+    vB = cv.take<int32_t>(N);
+    counts = cv.take<int>((int64_t)nb * ntiles);
+    totals = cv.take<int>(nb);
+    oob_tile = cv.take<int>(ntiles);
+    bstart = cv.take<int>(nb);
+  }
+};
+
+// Sort of (gen(coords[i]), i) for i < N (N > 0) by keys below 2^nbits, at most TBMAX bucket bits:
+// pack, scan, partition, buckets.  Sorted pairs go to (kOut, vOut), the column starts to cols
+// when it is not null (for the map's (b, x, y) columns of Z keys each), the out-of-range flag to
+// *status.  `tag` prefixes the profiler names.
+template <typename K, typename Gen>
+void sort_stages(tsc_ctx* ctx, const int32_t* coords, int64_t N, Gen gen, int nbits,
+                 const SortBufs<K>& sb, K* kOut, int32_t* vOut, int64_t cells, int64_t Z,
+                 int64_t ncol, int32_t* cols, uint32_t* status, const char* const names[4]) {
+  const int tb = std::min(nbits, TBMAX);
+  const int lb = nbits - tb;
+  const int nbk = 1 << tb;
+  const int64_t ntiles = (N + PTILE - 1) / PTILE;
+  hipStream_t s = ctx->stream;
+  {
+    ProfScope p(ctx, names[0]);
+    pack_kernel<K, Gen><<<(unsigned)ntiles, PT, 0, s>>>(
+        (const int4*)coords, N, gen, sb.kA, sb.vA, lb, tb, sb.counts, (int)ntiles, sb.oob_tile);
+  }
+  {
+    ProfScope ps(ctx, names[1]);
+    scan_kernel<<<(unsigned)nbk, RT, 0, s>>>(sb.counts, (int)ntiles, sb.totals, sb.oob_tile,
+                                             status);
+  }
+  {
+    ProfScope ps(ctx, names[2]);
+    partition_kernel<K><<<(unsigned)ntiles, PT, 0, s>>>(
+        sb.kA, sb.vA, N, lb, tb, sb.counts, sb.totals, (int)ntiles, sb.kB, sb.vB, sb.bstart);
+  }
+  {
+    ProfScope ps(ctx, names[3]);
+    bucket_sort_kernel<K><<<(unsigned)nbk, RT, 0, s>>>(sb.kB, sb.vB, sb.kA, sb.vA, kOut, vOut,
+                                                        sb.totals, sb.bstart, nbk, lb, cells, Z,
+                                                        ncol, N, cols);
+  }
+}
+
 template <typename K>
 int radix_impl(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t B, int32_t X, int32_t Y,
                int32_t Z, const int32_t dil[3], void* keys_out, int32_t* perm_out,
                int32_t* nbr_out, uint32_t* status_dev) {
   const int64_t cells = (int64_t)B * X * Y * Z;
   const int nbits = std::max(1, bit_length((uint64_t)(cells - 1)));
-  const int tb = std::min(nbits, TBMAX);
-  const int lb = nbits - tb;
-  const int nbk = 1 << tb;
-  const int64_t ntiles = (N + PTILE - 1) / PTILE;
   const int64_t ncol = (int64_t)B * X * Y;
   const bool use_cols = ncol <= std::max<int64_t>(16 * N, int64_t(1) << 22);
-  const int64_t S = (int64_t)nbk * ntiles;
-  size_t need = 2 * align_up((size_t)N * sizeof(K), 256) + 2 * align_up((size_t)N * 4, 256) +
-                align_up((size_t)S * 4, 256) + align_up(NBMAX * 4, 256) +
-                align_up((size_t)ntiles * 4, 256) + align_up(NBMAX * 4, 256) +
+  size_t need = SortBufs<K>::bytes(N, NBMAX) +
                 (use_cols ? align_up((size_t)(ncol + 1) * 4, 256) : 0);
   if (!keys_out) need += align_up((size_t)N * sizeof(K), 256);
   if (!perm_out) need += align_up((size_t)N * 4, 256);
@@ -938,14 +1071,8 @@ int radix_impl(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t B, int32_
   int st = workspace(ctx, need, &ws);
   if (st) return st;
   Carve cv(ws);
-  K* kA = cv.take<K>(N);
-  int32_t* vA = cv.take<int32_t>(N);
-  K* kB = cv.take<K>(N);
-  int32_t* vB = cv.take<int32_t>(N);
-  int* counts = cv.take<int>(S);
-  int* totals = cv.take<int>(NBMAX);
-  int* oob_tile = cv.take<int>(ntiles);
-  int* bstart = cv.take<int>(NBMAX);
+  SortBufs<K> sb;
+  sb.carve(cv, N, NBMAX);
   int32_t* cols = use_cols ? cv.take<int32_t>(ncol + 1) : nullptr;
   K* kOut = keys_out ? (K*)keys_out : cv.take<K>(N);
   int32_t* vOut = perm_out ? perm_out : cv.take<int32_t>(N);
@@ -955,27 +1082,10 @@ int radix_impl(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t B, int32_
     clear_status_kernel<<<1, 64, 0, s>>>(status_dev);
     return check_hip(hipGetLastError(), "map_build_radix launch");
   }
-  {
-    ProfScope p(ctx, "radix_pack");
-    pack_kernel<K><<<(unsigned)ntiles, PT, 0, s>>>((const int4*)coords, N, B, X, Y, Z,
-                                                    (K)(cells - 1), kA, vA, lb, tb, counts,
-                                                    (int)ntiles, oob_tile);
-  }
-  {
-    ProfScope ps(ctx, "radix_scan");
-    scan_kernel<<<(unsigned)nbk, RT, 0, s>>>(counts, (int)ntiles, totals, oob_tile, status_dev);
-  }
-  {
-    ProfScope ps(ctx, "radix_partition");
-    partition_kernel<K><<<(unsigned)ntiles, PT, 0, s>>>(kA, vA, N, lb, tb, counts, totals,
-                                                         (int)ntiles, kB, vB, bstart);
-  }
-  {
-    ProfScope ps(ctx, "radix_buckets");
-    bucket_sort_kernel<K><<<(unsigned)nbk, RT, 0, s>>>(kB, vB, kA, vA, kOut, vOut, totals,
-                                                        bstart, nbk,
-                                                        lb, cells, Z, ncol, N, cols);
-  }
+  static const char* const names[4] = {"radix_pack", "radix_scan", "radix_partition",
+                                       "radix_buckets"};
+  sort_stages<K>(ctx, coords, N, PackedKey<K>{B, X, Y, Z, (K)(cells - 1)}, nbits, sb, kOut, vOut,
+                 cells, Z, ncol, cols, status_dev, names);
   {
     ProfScope ps(ctx, "radix_fill");
     const K no_sentinel = (K)-1;  // out-of-range voxels were clamped in pack
@@ -1008,6 +1118,42 @@ int map_build_radix(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t B, i
                                status_dev);
   return radix_impl<int64_t>(ctx, coords, N, B, X, Y, Z, dil, keys_out, perm_out, nbr_out,
                              status_dev);
+}
+
+namespace {
+
+// Morton keys of up to 32 bits sort as uint32, wider ones as uint64.  A 512^3 shell's Z-curve puts
+// up to 12 k voxels under one 10-bit prefix; the bucket kernel's bitmap rank takes them in chunks
+// (measured on that shell: 10 bucket bits 68 us for the four stages, 12 bits 86 us, where the
+// larger partition and pack histograms cost more than the smaller buckets save).
+template <typename K>
+int morton_impl(tsc_ctx* ctx, const int32_t* coords, int64_t N, int bits, int shift, int nbits,
+                int32_t* rows_out) {
+  const size_t need = SortBufs<K>::bytes(N, NBMAX) + align_up((size_t)N * sizeof(K), 256) +
+                      256;
+  void* ws;
+  int st = workspace(ctx, need, &ws);
+  if (st) return st;
+  Carve cv(ws);
+  SortBufs<K> sb;
+  sb.carve(cv, N, NBMAX);
+  K* kOut = cv.take<K>(N);
+  uint32_t* status = cv.take<uint32_t>(1);  // the scan's flag word; Morton keys never set it
+  const uint64_t mask = nbits >= 64 ? ~0ull : ((1ull << nbits) - 1);
+  static const char* const names[4] = {"morton_pack", "morton_scan", "morton_partition",
+                                       "morton_buckets"};
+  sort_stages<K>(ctx, coords, N, MortonKey<K>{bits, shift, mask}, nbits, sb, kOut, rows_out,
+                 (int64_t)0, (int64_t)1, (int64_t)0, nullptr, status, names);
+  return check_hip(hipGetLastError(), "gather plan sort");
+}
+
+}  // namespace
+
+int sort_rows_morton(tsc_ctx* ctx, const int32_t* coords, int64_t N, int bits, int shift,
+                     int nbits, int32_t* rows_out) {
+  if (N == 0) return TSC_OK;
+  return nbits <= 32 ? morton_impl<uint32_t>(ctx, coords, N, bits, shift, nbits, rows_out)
+                     : morton_impl<uint64_t>(ctx, coords, N, bits, shift, nbits, rows_out);
 }
 
 }  // namespace tsc

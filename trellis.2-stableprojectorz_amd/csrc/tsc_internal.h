@@ -99,6 +99,11 @@ int map_build_bitmap(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t B, 
 int map_build_radix(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t B, int32_t X,
                     int32_t Y, int32_t Z, const int32_t dil[3], void* keys_out, int32_t* perm_out,
                     int32_t* nbr_out, uint32_t* status_dev);
+// Rows 0..N-1 sorted by the (batch, Z-curve) key of their coordinates over the low `bits` bits of
+// x, y, z (z lowest), the lowest `shift` bits dropped, nbits = key width (<= 64); the radix sort
+// of map_build_radix with a Morton key.  Writes rows_out[0..N).
+int sort_rows_morton(tsc_ctx* ctx, const int32_t* coords, int64_t N, int bits, int shift,
+                     int nbits, int32_t* rows_out);
 
 // ---- launcher implemented in conv_order.hip ----
 int conv_order_launch(tsc_ctx* ctx, const int32_t* nbr, const int32_t* perm, int64_t N,

@@ -53,11 +53,14 @@ def short_name(name: str) -> str:
     m = re.search(r"(?:tsc::\(anonymous namespace\)::|N_1\d+)(\w+_kernel)", name)
     if m:
         base = m.group(1)
-        tm = re.search(r"<(int|long)", name)
+        # key types: int32/int64 for the neighbor map's sort, uint32/uint64 for the gather plan's
+        # Morton sort
+        tm = re.search(r"<(unsigned int|unsigned long|int|long)", name)
         if "fill_columns_kernel" in name:
             base += "<radix>" if "ColumnLookup" in name else "<bitmap>"
         elif tm:
-            base += f"<{'int32' if tm.group(1) == 'int' else 'int64'}>"
+            base += "<" + {"int": "int32", "long": "int64", "unsigned int": "uint32",
+                           "unsigned long": "uint64"}[tm.group(1)] + ">"
         return base
     m = re.search(r"(layernorm\w*_kernel|silu_kernel|add_kernel)", name)
     if m:
