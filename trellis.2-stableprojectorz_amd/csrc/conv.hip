@@ -371,7 +371,7 @@ __global__ void __launch_bounds__(64 * WM * WN)
   // weight row W[co, v, :] for B pieces.  Within a tap a chunk only adds its Ci offset.
   const char* gsrc[C::IPW];
   int is_tap = -1, is_k = cpt - 1;
-  auto issue = [&](unsigned char* sbase) {
+  auto advance = [&]() {
     if (++is_k == cpt) {
       is_k = 0;
       ++is_tap;
@@ -400,18 +400,28 @@ __global__ void __launch_bounds__(64 * WM * WN)
         gsrc[j] = isA ? ga : gb;
       }
     }
-    const int off = is_k * KB;  // bytes into the rows for this chunk's Ci slice
+  };
+  // Load instruction j of the current chunk (after advance()) into stage sbase.
+  auto dma = [&](int j, unsigned char* sbase) {
+    if (C::PPW % 64 == 0 || j * 64 + lane < C::PPW)
+      lds_dma16(gsrc[j] + is_k * KB, (lds_ptr_t)(sbase + (wid * C::PPW + j * 64) * 16));
+  };
+  auto issue = [&](unsigned char* sbase) {
+    advance();
 #pragma unroll
-    for (int j = 0; j < C::IPW; ++j)
-      if (C::PPW % 64 == 0 || j * 64 + lane < C::PPW)
-        lds_dma16(gsrc[j] + off, (lds_ptr_t)(sbase + (wid * C::PPW + j * 64) * 16));
+    for (int j = 0; j < C::IPW; ++j) dma(j, sbase);
   };
 
   // MFMA over one stage.  Fragments are read with inline-asm ds_read_b128 and an explicit
   // lgkmcnt wait: the compiler sees no LDS read of the ring, so it adds no vmcnt wait for the
   // DMA loads still in flight into the other stages.
-  auto compute = [&](const unsigned char* sA) {
+  // With nxt set, the next chunk's loads into stage nxt are spread over the micro-steps, each
+  // group issued after that micro-step's MFMAs: the wave never stalls on a full load queue
+  // ahead of its MFMAs (issuing all of a chunk's loads up front left the matrix pipe idle).
+  auto compute = [&](const unsigned char* sA, unsigned char* nxt) {
     const uint32_t a0 = lds_addr(sA), b0 = a0 + C::A_PIECES * 16;
+    if (nxt) advance();
+    constexpr int JPS = (C::IPW + C::MS - 1) / C::MS;  // loads per micro-step
 #pragma unroll
     for (int s = 0; s < C::MS; ++s) {
       const int part = 2 * s + (lane >> 5);
@@ -437,6 +447,11 @@ __global__ void __launch_bounds__(64 * WM * WN)
         for (int j = 0; j < C::FN; ++j)
           mfma_piece<T>(__builtin_bit_cast(uint4, a[i]), __builtin_bit_cast(uint4, b[j]),
                         acc[i][j]);
+      if (nxt) {
+#pragma unroll
+        for (int j = s * JPS; j < (s + 1) * JPS; ++j)
+          if (j < C::IPW) dma(j, nxt);
+      }
     }
   };
 
@@ -462,8 +477,7 @@ __global__ void __launch_bounds__(64 * WM * WN)
         TSC_COMPILER_BARRIER();
         __builtin_amdgcn_s_barrier();
         TSC_COMPILER_BARRIER();
-        if (c + STAGES - 1 < nchunks) issue(ring[(s + STAGES - 1) % STAGES]);
-        compute(ring[s]);
+        compute(ring[s], c + STAGES - 1 < nchunks ? ring[(s + STAGES - 1) % STAGES] : nullptr);
       }
     }
   }
