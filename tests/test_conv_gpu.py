@@ -156,9 +156,9 @@ def test_conv_order_invariance_bit_exact(pkg, dev, dtype):
 
 @pytest.mark.parametrize("workload", ["map512", "wide128_bf16", "conv64_f32"])
 def test_map_conv_order(pkg, dev, workload):
-    """The conv order: inside each window of 262144 consecutive key-sorted rows, rows sorted by their
-    26-bit mask of present neighbors (corner taps in the top bits, then edges, then faces, each
-    class in tap order; tap 13 left out), ties in key order."""
+    """The conv order: inside each window of 262144 consecutive key-sorted rows, rows sorted by the
+    Gray-sequence rank of their 26-bit mask of present neighbors (corner taps in the top bits, then
+    edges, then faces, each class in tap order; tap 13 left out), ties in key order."""
     coords = pkg.workloads.make_coords(workload)
     batch = int(coords[:, 0].max()) + 1
     m = _map(pkg, dev, coords, batch, pkg.workloads.grid_shape(workload))
@@ -174,6 +174,13 @@ def test_map_conv_order(pkg, dev, workload):
     m26 = np.zeros(n, np.int64)
     for v in taps:
         m26 = (m26 << 1) | present[:, v]
+    # rank of m26 read as a reflected binary (Gray) code: bit i of the rank is the XOR of bits
+    # i..25 of the code
+    rank = np.zeros(n, np.int64)
+    for i in range(26):
+        rank |= (np.bitwise_xor.reduce([(m26 >> j) & 1 for j in range(i, 26)], axis=0)) << i
+    assert rank[m26 == 0].max(initial=0) == 0
+    m26 = rank
     want = np.empty(n, np.int64)
     win = 262144
     for w0 in range(0, n, win):

@@ -6,8 +6,9 @@
 // multiplication by absent (zero) rows.  The order sorts rows inside windows of 262144
 // consecutive key-sorted rows (spatially grouped, so gathers keep some locality) by their 26-bit
 // mask of present neighbors (corner taps in the top bits, then edges, then faces; tap 13, the
-// row itself, is always present): numeric order puts masks that share their leading taps next to
-// each other, so a tile's union of taps stays close to one row's.  Ties keep key order.
+// row itself, is always present), ranked in the reflected binary (Gray) sequence: masks that share
+// their leading taps sit next to each other, and consecutive ones differ in as few taps as the
+// sequence allows, so a tile's union of taps stays close to one row's.  Ties keep key order.
 //
 // Stable LSD radix sort, three passes of <= 9 bits, over tiles of 16384 rows (16 per window):
 //   mask     key = mask of row perm[i], val = perm[i]; tile histogram of digit 0
@@ -18,8 +19,9 @@
 //   hist     tile histogram of the next digit
 // Processed taps / valid taps (CPU model of the tiles) on the 2-voxel shells in 128^3 with
 // 256-row tiles: key order 1.65, 65536-row windows with taps in index order 1.36, corner-first
-// 1.28, 262144-row windows 1.18 (the wide conv measured 6 % faster than with 65536); on the
-// 1-voxel 512^3 shell with 32-row tiles: 1.13 (65536) and 1.05 (262144).
+// 1.28, 262144-row windows 1.18 (the wide conv measured 6 % faster than with 65536), Gray rank
+// 1.166 (2 x 30k-voxel shells in 64^3: 1.344 -> 1.324); on the 1-voxel 512^3 shell with 32-row
+// tiles: 1.13 (65536), 1.049 (262144), 1.044 (Gray rank).
 
 #include <utility>
 
@@ -83,6 +85,13 @@ __global__ void __launch_bounds__(kOrdThreads)
       uint32_t m = 0;
 #pragma unroll
       for (int k = 0; k < kOrdMaskBits; ++k) m = (m << 1) | (uint32_t)(nr[kMaskTap[k]] >= 0);
+      // Sort by the mask's position in the reflected binary (Gray) sequence: neighbors in that
+      // sequence differ in one tap, where numeric neighbors can differ in many low taps.
+      m ^= m >> 1;
+      m ^= m >> 2;
+      m ^= m >> 4;
+      m ^= m >> 8;
+      m ^= m >> 16;
       keys[i] = m;
       vals[i] = r;
       atomicAdd(&hist[digit(m, 0)], 1);
