@@ -158,7 +158,9 @@ def test_conv_order_invariance_bit_exact(pkg, dev, dtype):
 def test_map_conv_order(pkg, dev, workload):
     """The conv order: inside each window of 262144 consecutive key-sorted rows, rows sorted by the
     Gray-sequence rank of their 26-bit mask of present neighbors (corner taps in the top bits, then
-    edges, then faces, each class in tap order; tap 13 left out), ties in key order."""
+    edges, then faces, each class in tap order; tap 13 left out), ties in key order; then inside
+    each chunk of 4096 sorted rows, 256-row tiles regrouped greedily (_greedy_tiles).  Exact
+    match, and the regrouping never raises the taps the 256-row tiles process."""
     coords = pkg.workloads.make_coords(workload)
     batch = int(coords[:, 0].max()) + 1
     m = _map(pkg, dev, coords, batch, pkg.workloads.grid_shape(workload))
@@ -181,12 +183,72 @@ def test_map_conv_order(pkg, dev, workload):
         rank |= (np.bitwise_xor.reduce([(m26 >> j) & 1 for j in range(i, 26)], axis=0)) << i
     assert rank[m26 == 0].max(initial=0) == 0
     m26 = rank
-    want = np.empty(n, np.int64)
+    srt = np.empty(n, np.int64)
     win = 262144
     for w0 in range(0, n, win):
         rows = perm[w0:w0 + win]
-        want[w0:w0 + win] = rows[np.argsort(m26[rows], kind="stable")]
+        srt[w0:w0 + win] = rows[np.argsort(m26[rows], kind="stable")]
+    want = _greedy_tiles(srt, m26[srt])
     np.testing.assert_array_equal(order, want)
+    assert np.array_equal(np.sort(order), np.arange(n))
+    mask = (m26 ^ (m26 >> 1))[order], (m26 ^ (m26 >> 1))[srt]  # neighbor masks (ranks -> codes)
+    taps = [_tile_taps(x, 256) for x in mask]
+    assert taps[0] <= taps[1], taps
+
+
+def _popcount(a):
+    a = np.asarray(a, np.int64)
+    c = np.zeros_like(a)
+    for b in range(26):
+        c += (a >> b) & 1
+    return c
+
+
+def _tile_taps(masks, tile):
+    """Taps processed by `tile`-row tiles: popcount of each tile's OR, times the tile's rows."""
+    t = (len(masks) + tile - 1) // tile
+    pad = np.zeros(t * tile, np.int64)
+    pad[:len(masks)] = masks
+    return int((_popcount(np.bitwise_or.reduce(pad.reshape(t, tile), axis=1)) * tile).sum())
+
+
+def _greedy_tiles(srt, rank, chunk=4096, tile=256):
+    """Greedy 256-row tiles inside each chunk of the sorted rows `srt` (Gray ranks `rank`): entries
+    = runs of equal rank, ordered by run length capped at 255 (descending), then rank; a tile starts from the
+    first entry with rows left (OR = its mask) and takes, in entry order, the rows of every entry
+    whose mask lies inside OR; while rows are missing, OR gains the entry mask that adds the fewest
+    taps (lowest entry on ties).  Rows of an entry are taken in their sorted order."""
+    out = np.empty_like(srt)
+    for c0 in range(0, len(srt), chunk):
+        rows, rk = srt[c0:c0 + chunk], rank[c0:c0 + chunk]
+        nc = len(rows)
+        heads = np.flatnonzero(np.r_[True, rk[1:] != rk[:-1]])
+        cnt = np.diff(np.r_[heads, nc])
+        o = np.lexsort((rk[heads], -np.minimum(cnt, 255)))
+        mask = rk[heads][o] ^ (rk[heads][o] >> 1)
+        pos, left = heads[o].copy(), cnt[o].copy()
+        ptr = 0
+        for t0 in range(0, nc, tile):
+            need = min(tile, nc - t0)
+            src = []
+            while left[ptr] == 0:
+                ptr += 1
+            orm = int(mask[ptr])
+            while True:
+                for i in np.flatnonzero((left > 0) & ((mask & ~orm) == 0)):
+                    take = int(min(left[i], need))
+                    src.extend(range(pos[i], pos[i] + take))
+                    pos[i] += take
+                    left[i] -= take
+                    need -= take
+                    if need == 0:
+                        break
+                if need == 0:
+                    break
+                alive = np.flatnonzero(left > 0)
+                orm |= int(mask[alive[np.argmin(_popcount(mask[alive] & ~orm))]])
+            out[c0 + t0:c0 + t0 + len(src)] = rows[np.asarray(src)]
+    return out
 
 
 def test_conv_properties(pkg, dev):

@@ -23,6 +23,7 @@
 // 1.166 (2 x 30k-voxel shells in 64^3: 1.344 -> 1.324); on the 1-voxel 512^3 shell with 32-row
 // tiles: 1.13 (65536), 1.049 (262144), 1.044 (Gray rank).
 
+#include <climits>
 #include <utility>
 
 #include "tsc_internal.h"
@@ -212,6 +213,265 @@ __global__ void __launch_bounds__(kOrdThreads)
   }
 }
 
+// Greedy tile grouping inside chunks of kGrChunk rows of the mask-sorted order (one block per
+// chunk).  The sort alone leaves tiles that straddle many short runs of distinct masks (on the
+// 2-voxel shells ~16 k distinct masks for 64-243 k rows); this pass rebuilds each 256-row tile
+// around one popular mask and the masks contained in it:
+//   entries  the chunk's runs of equal masks, ordered by row count capped at 255 (descending),
+//            then by the sort key; each keeps its next unused position and its remaining rows
+//   tile     seed = the first entry with rows left; OR = its mask.  Repeat: take rows, in entry
+//            order, from every entry whose mask lies inside OR, until the tile is full; if rows
+//            are still missing, add to OR the entry mask that brings the fewest new taps (lowest
+//            entry index on ties) and take again.  Every added mask brings at least one new tap,
+//            so a tile completes after at most 26 growths.
+// Chunks of consecutive sorted rows share their leading taps, so grouping inside a chunk loses
+// little against one pool of all rows (processed / valid taps with 256-row tiles on the 2-voxel
+// shells: sorted 1.166 / 1.324, chunks of 4096 1.112 / 1.227, of 8192 1.107 / 1.222, one pool
+// 1.101 / 1.213; a block's passes run one after another, so 4096-row chunks halve the kernel's
+// critical path for +0.5 % of taps; the count cap changes nothing measurable and makes the
+// entry order an 8-bit stable counting sort).
+// Thread t owns entries [t*E, t*E + E) in registers throughout the tile loop, so a pass over the
+// entries is register work plus two block reductions.
+constexpr int kGrChunk = 4096;   // rows per chunk (and at most this many entries)
+constexpr int kGrThreads = 1024;
+constexpr int kGrTile = 256;     // rows per tile of the 256-row conv kernels
+constexpr int kGrPerThread = kGrChunk / kGrThreads;  // rows, and entries at most, per thread
+static_assert(kOrdTilesPerWin * kOrdTile % kGrChunk == 0, "chunks never straddle a window");
+static_assert(kGrChunk % kGrTile == 0, "chunks hold whole tiles");
+static_assert(kGrTile <= kGrThreads, "one thread per tile slot");
+
+// Entry state: mask (26 bits) | next position in the chunk << 26 | rows left << 40.  Positions
+// and counts reach kGrChunk itself (a run that ends the chunk), so each field has 14 bits.
+static_assert(kGrChunk < (1 << 14), "14-bit position and count fields");
+__device__ __forceinline__ uint32_t gr_mask(uint64_t e) { return (uint32_t)(e & 0x3ffffffu); }
+__device__ __forceinline__ int gr_pos(uint64_t e) { return (int)((e >> 26) & 0x3fffu); }
+__device__ __forceinline__ int gr_left(uint64_t e) { return (int)(e >> 40); }
+__device__ __forceinline__ uint64_t gr_make(uint32_t mask, int pos, int left) {
+  return (uint64_t)mask | ((uint64_t)pos << 26) | ((uint64_t)left << 40);
+}
+
+// Inclusive wave64 scans on DPP lane moves (row_shr inside each 16-lane row, then row_bcast:15
+// and row_bcast:31 across rows); lanes whose source is outside the row keep the identity.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ int dpp_mov(int old, int x) {
+  return __builtin_amdgcn_update_dpp(old, x, CTRL, ROWS, 0xf, false);
+}
+__device__ __forceinline__ int wave_incl_add(int x) {
+  x += dpp_mov<0x111, 0xf>(0, x);  // row_shr:1
+  x += dpp_mov<0x112, 0xf>(0, x);  // row_shr:2
+  x += dpp_mov<0x114, 0xf>(0, x);  // row_shr:4
+  x += dpp_mov<0x118, 0xf>(0, x);  // row_shr:8
+  x += dpp_mov<0x142, 0xa>(0, x);  // row_bcast:15 into rows 1 and 3
+  x += dpp_mov<0x143, 0xc>(0, x);  // row_bcast:31 into rows 2 and 3
+  return x;
+}
+__device__ __forceinline__ uint32_t umin32(uint32_t a, uint32_t b) { return a < b ? a : b; }
+__device__ __forceinline__ uint32_t wave_incl_umin(uint32_t x) {
+  const int m = -1;  // identity: 0xffffffff
+  x = umin32(x, (uint32_t)dpp_mov<0x111, 0xf>(m, (int)x));
+  x = umin32(x, (uint32_t)dpp_mov<0x112, 0xf>(m, (int)x));
+  x = umin32(x, (uint32_t)dpp_mov<0x114, 0xf>(m, (int)x));
+  x = umin32(x, (uint32_t)dpp_mov<0x118, 0xf>(m, (int)x));
+  x = umin32(x, (uint32_t)dpp_mov<0x142, 0xa>(m, (int)x));
+  x = umin32(x, (uint32_t)dpp_mov<0x143, 0xc>(m, (int)x));
+  return x;
+}
+__device__ __forceinline__ int wave_incl_max(int x) {  // x >= -1
+  x = max(x, dpp_mov<0x111, 0xf>(-1, x));
+  x = max(x, dpp_mov<0x112, 0xf>(-1, x));
+  x = max(x, dpp_mov<0x114, 0xf>(-1, x));
+  x = max(x, dpp_mov<0x118, 0xf>(-1, x));
+  x = max(x, dpp_mov<0x142, 0xa>(-1, x));
+  x = max(x, dpp_mov<0x143, 0xc>(-1, x));
+  return x;
+}
+
+// Sort digit of entry e (runs in run order: head[e] = first position): 255 - min(rows, 255).
+__device__ __forceinline__ int gr_digit(const int32_t* head, int e) {
+  const int rows = head[e + 1] - head[e];
+  return 255 - (rows < 255 ? rows : 255);
+}
+
+__global__ void __launch_bounds__(kGrThreads)
+    ord_greedy_kernel(const uint32_t* __restrict__ keys, const int32_t* __restrict__ vals,
+                      int64_t n, int32_t* __restrict__ order) {
+  __shared__ int32_t head[kGrChunk + 1];  // run starts; later the tile's segment marks
+  __shared__ int32_t idxa[kGrChunk];      // entry order (sort); later each output slot's source
+  __shared__ int32_t buf[8 * kGrThreads + kGrChunk];  // sort counters | entry order; later masks
+  __shared__ int wsum[kGrThreads / 64];
+  __shared__ int wmax[kGrThreads / 64];
+  __shared__ int wtot[2][kGrThreads / 64];        // per-pass wave sums (two buffers by parity)
+  __shared__ uint32_t wbest[2][kGrThreads / 64];  // per-pass wave minima
+  __shared__ uint32_t wseed[kGrThreads / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int64_t c0 = (int64_t)blockIdx.x * kGrChunk;
+  const int nc = (int)(n - c0 < kGrChunk ? n - c0 : kGrChunk);
+
+  // Runs of equal keys: thread t owns positions [t*P, t*P + P).
+  int nd;
+  {
+    uint32_t hb = 0;  // bit j: position p0 + j starts a run
+    const int p0 = tid * kGrPerThread;
+    uint32_t prev = p0 > 0 && p0 <= nc ? keys[c0 + p0 - 1] : 0u;
+#pragma unroll
+    for (int j = 0; j < kGrPerThread; ++j) {
+      const int i = p0 + j;
+      const uint32_t k = i < nc ? keys[c0 + i] : 0u;
+      hb |= (i < nc && (i == 0 || k != prev) ? 1u : 0u) << j;
+      prev = k;
+    }
+    int e = block_excl_scan(__popc(hb), wsum, kGrThreads / 64);
+    nd = 0;
+#pragma unroll
+    for (int ww = 0; ww < kGrThreads / 64; ++ww) nd += wsum[ww];
+    for (uint32_t m = hb; m; m &= m - 1) head[e++] = p0 + __ffs(m) - 1;
+    if (tid == 0) head[nd] = nc;
+  }
+  // Entries per thread: contiguous runs [ebeg, ebeg + ne).
+  const int E = (nd + kGrThreads - 1) / kGrThreads;
+  const int ebeg = tid * E;
+  const int ne = max(0, min(nd - ebeg, E));
+  for (int i = tid; i < nd; i += kGrThreads) idxa[i] = i;
+  __syncthreads();
+  // Stable LSD counting sort of the entries by gr_digit, three passes of 3 bits: per-thread digit
+  // counts in a digit-major [8][kGrThreads] matrix, one block scan, stable placement; the passes
+  // alternate between idxa and idxb and end in idxb.
+  constexpr int kDig = 8, kCpt = kDig * kGrThreads / kGrThreads;  // counters per thread in the scan
+  int32_t* const cnt = buf;  // [kDig][kGrThreads]
+  int32_t* const idxb = buf + kDig * kGrThreads;
+  static_assert(kDig == 8 && kGrChunk <= kDig * kGrThreads, "counters, order and masks fit buf");
+  for (int pass = 0; pass < 3; ++pass) {
+    const int32_t* src = (pass & 1) ? idxb : idxa;
+    int32_t* dst = (pass & 1) ? idxa : idxb;
+    const int sh = 3 * pass;
+    // column tid of the counter matrix belongs to this thread alone
+    for (int d = 0; d < kDig; ++d) cnt[d * kGrThreads + tid] = 0;
+    for (int j = 0; j < ne; ++j)
+      ++cnt[((gr_digit(head, src[ebeg + j]) >> sh) & (kDig - 1)) * kGrThreads + tid];
+    __syncthreads();
+    // exclusive scan of the counters in digit-major order: thread t scans [t*kCpt, t*kCpt + kCpt)
+    int sum = 0;
+    for (int q = 0; q < kCpt; ++q) sum += cnt[tid * kCpt + q];
+    int pre = block_excl_scan(sum, wsum, kGrThreads / 64);
+    for (int q = 0; q < kCpt; ++q) {
+      const int c = cnt[tid * kCpt + q];
+      cnt[tid * kCpt + q] = pre;
+      pre += c;
+    }
+    __syncthreads();
+    for (int j = 0; j < ne; ++j) {
+      const int e = src[ebeg + j];
+      dst[cnt[((gr_digit(head, e) >> sh) & (kDig - 1)) * kGrThreads + tid]++] = e;
+    }
+    __syncthreads();
+  }
+  // This thread's entries (sorted positions ebeg..ebeg+ne) into registers; masks to LDS.
+  uint64_t my[kGrPerThread];
+#pragma unroll
+  for (int j = 0; j < kGrPerThread; ++j) {
+    my[j] = 0;
+    if (j < ne) {
+      const int e = idxb[ebeg + j];
+      const int a = head[e];
+      const uint32_t rank = keys[c0 + a];
+      my[j] = gr_make(rank ^ (rank >> 1), a, head[e + 1] - a);
+    }
+  }
+  __syncthreads();
+  uint32_t* const emask = (uint32_t*)buf;
+#pragma unroll
+  for (int j = 0; j < kGrPerThread; ++j)
+    if (j < ne) emask[ebeg + j] = gr_mask(my[j]);
+  // Segment marks of a tile (the run starts are no longer needed): a taking entry marks the
+  // first tile slot it fills with (its source position - that slot + kMarkOff); the slots after
+  // it up to the next mark come from the same run.
+  int32_t* const mark = head;
+  int32_t* const srcpos = idxa;
+  constexpr int kMarkOff = 1 << 16;
+  const int ntile = (nc + kGrTile - 1) / kGrTile;
+  for (int t = 0; t < ntile; ++t) {
+    const int rows = min(kGrTile, nc - t * kGrTile);
+    if (tid < kGrTile) mark[tid] = 0;
+    // seed: the first entry with rows left
+    uint32_t fa = ~0u;
+#pragma unroll
+    for (int j = kGrPerThread - 1; j >= 0; --j)
+      if (j < ne && gr_left(my[j]) > 0) fa = (uint32_t)(ebeg + j);
+    fa = wave_incl_umin(fa);
+    if (lane == 63) wseed[wid] = fa;
+    __syncthreads();
+#pragma unroll
+    for (int ww = 0; ww < kGrThreads / 64; ++ww) fa = umin32(fa, wseed[ww]);
+    uint32_t orm = emask[fa];  // rows remain, so an entry with rows exists
+    int need = rows, fill = 0;
+    for (int iter = 0;; ++iter) {
+      if (iter >= 27) orm = ~0u;  // 26 growths fill OR; guard only
+      // One block reduction per pass: the rows of the entries inside OR (to be taken, in entry
+      // order) and, among the other entries with rows left, the one whose mask adds the fewest
+      // taps (lowest index on ties) -- the growth if the tile is still short.  Taking touches
+      // only entries inside OR, so the growth candidate stays valid after it.
+      int sum = 0;
+      uint32_t cand = ~0u;
+#pragma unroll
+      for (int j = 0; j < kGrPerThread; ++j) {
+        const int left = gr_left(my[j]);
+        if (j < ne && left > 0) {
+          const uint32_t out = gr_mask(my[j]) & ~orm;
+          if (out == 0u) sum += left;
+          else cand = umin32(cand, ((uint32_t)__popc(out) << 14) | (uint32_t)(ebeg + j));
+        }
+      }
+      const int incl = wave_incl_add(sum);
+      const uint32_t wmin = wave_incl_umin(cand);
+      int* const wt = wtot[iter & 1];
+      uint32_t* const wb = wbest[iter & 1];
+      if (lane == 63) {
+        wt[wid] = incl;
+        wb[wid] = wmin;
+      }
+      __syncthreads();
+      int o = incl - sum, tot = 0;
+      uint32_t best = ~0u;
+#pragma unroll
+      for (int ww = 0; ww < kGrThreads / 64; ++ww) {
+        const int v = wt[ww];
+        tot += v;
+        o += ww < wid ? v : 0;
+        best = umin32(best, wb[ww]);
+      }
+#pragma unroll
+      for (int j = 0; j < kGrPerThread; ++j) {
+        const int left = gr_left(my[j]);
+        if (j < ne && left > 0 && (gr_mask(my[j]) & ~orm) == 0u && o < need) {
+          const int take = min(left, need - o);
+          const int pos = gr_pos(my[j]);
+          mark[fill + o] = pos - (fill + o) + kMarkOff;
+          my[j] = gr_make(gr_mask(my[j]), pos + take, left - take);
+          o += left;
+        }
+      }
+      const int got = min(tot, need);
+      fill += got;
+      need -= got;
+      if (need == 0) break;
+      orm |= best != ~0u ? emask[best & 0x3fffu] : ~0u;
+    }
+    __syncthreads();  // marks of every thread
+    // Slot r takes its source from the last mark at or before r (inclusive max scan of the
+    // marked slots over the tile's 256 slots, waves 0..3).
+    {
+      int last = wave_incl_max((tid < kGrTile && mark[tid] != 0) ? tid : -1);
+      if (lane == 63) wmax[wid] = last;
+      __syncthreads();
+      for (int ww = 0; ww < wid && ww < kGrTile / 64; ++ww) last = max(last, wmax[ww]);
+      if (tid < rows) srcpos[t * kGrTile + tid] = tid + mark[last] - kMarkOff;
+      __syncthreads();
+    }
+  }
+  for (int i = tid; i < nc; i += kGrThreads) order[c0 + i] = vals[c0 + srcpos[i]];
+}
+
+
 }  // namespace
 
 int conv_order_launch(tsc_ctx* ctx, const int32_t* nbr, const int32_t* perm, int64_t N,
@@ -239,15 +499,14 @@ int conv_order_launch(tsc_ctx* ctx, const int32_t* nbr, const int32_t* perm, int
   for (int pass = 0; pass < kOrdPasses; ++pass) {
     const int shift = pass * kOrdDigitBits;
     const int dbits = kOrdMaskBits - shift < kOrdDigitBits ? kOrdMaskBits - shift : kOrdDigitBits;
-    const bool last = pass == kOrdPasses - 1;
     if (pass > 0) ord_hist_kernel<<<ntiles, kOrdThreads, 0, s>>>(kc, N, shift, counts);
     ord_scan_kernel<<<nwin, kOrdBins, 0, s>>>(counts, ntiles, offs);
-    ord_scatter_kernel<<<ntiles, kOrdThreads, 0, s>>>(kc, vc, N, shift, dbits, offs,
-                                                      last ? nullptr : kn,
-                                                      last ? order : vn);
+    ord_scatter_kernel<<<ntiles, kOrdThreads, 0, s>>>(kc, vc, N, shift, dbits, offs, kn, vn);
     std::swap(kc, kn);
     std::swap(vc, vn);
   }
+  ord_greedy_kernel<<<(unsigned)((N + kGrChunk - 1) / kGrChunk), kGrThreads, 0, s>>>(kc, vc, N,
+                                                                                     order);
   return check_hip(hipGetLastError(), "conv_order launch");
 }
 
