@@ -149,7 +149,10 @@ int tsc_conv(tsc_ctx* ctx, int32_t dtype, const void* feats, const void* weight,
              const int32_t* nbr, const int32_t* order, int64_t N, int32_t Ci, int32_t Co, void* out);
 
 /* tsc_conv followed by an epilogue.  residual (N,Co) is read for TSC_EPI_BIAS_RESIDUAL;
- * ln_gamma / ln_beta (Co, dtype, NULL = 1 / 0) and eps for TSC_EPI_BIAS_LN_SILU.
+ * ln_gamma / ln_beta (Co, dtype, NULL = 1 / 0) and eps for TSC_EPI_BIAS_LN_SILU, which runs
+ * inside the conv kernel when one block owns whole rows (fp16/bf16, Ci * 2 > 64 bytes, Co = 64,
+ * or Co = 128 / 256 with Ci * 2 a multiple of 64 bytes; 16-byte aligned gamma / beta) and as a
+ * LayerNorm row pass after it otherwise; the results are the same bits either way.
  * out may alias residual. */
 int tsc_conv_fused(tsc_ctx* ctx, int32_t dtype, const void* feats, const void* weight,
                    const void* bias, const int32_t* nbr, const int32_t* order, int64_t N,

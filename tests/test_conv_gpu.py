@@ -329,6 +329,43 @@ def test_conv_any_channels(pkg, dev, dtype, ci, co):
     assert rel_err(out.float().cpu().numpy(), ref) <= TOL[dtype] * (2 if co < 8 else 1)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("ci,co,fused", [(64, 64, True), (48, 64, True), (128, 128, True),
+                                         (256, 256, True), (48, 128, False), (64, 512, False)])
+def test_conv_ln_silu_epilogue_in_kernel(pkg, dev, dtype, ci, co, fused):
+    """Where the conv kernel owns whole output rows (16-bit rows wider than 64 bytes; Co = 64, or
+    Co = 128 / 256 with 64-byte K chunks) LayerNorm + SiLU run in its epilogue and no row pass is
+    launched; elsewhere the row pass runs.  Either way the result equals the conv followed by the
+    LayerNorm row pass bit for bit (with and without gamma / beta), and the fp64 oracle within
+    2e-2."""
+    coords, m = _small_map(pkg, dev, 5000)
+    n = len(coords)
+    nbr = m.nbr.cpu().numpy()
+    print(f"  conv LN epilogue N={n} {ci}->{co} {dtype}", flush=True)
+    f, f64 = _rounded(pkg.workloads.features(n, ci, ci), dtype, dev)
+    w, w64 = _rounded(pkg.workloads.conv_weight(co, ci, co), dtype, dev)
+    b, b64 = _rounded(np.linspace(-0.5, 0.5, co).astype(np.float32), dtype, dev)
+    g, g64 = _rounded(np.linspace(0.5, 1.5, co).astype(np.float32), dtype, dev)
+    be, be64 = _rounded(np.linspace(-0.2, 0.3, co).astype(np.float32), dtype, dev)
+    ctx = pkg._lib.context(dev.index)
+    m.conv_order()
+    torch.cuda.synchronize()
+    ctx.profile_reset()
+    ctx.profile(True)
+    out = pkg.sparse_conv3d(f, w, b, m, epilogue="ln_silu", ln_weight=g, ln_bias=be, eps=1e-6)
+    ctx.profile(False)
+    names = list(ctx.profile_results())
+    ctx.profile_reset()
+    assert any(",ln>" in k for k in names) == fused, names
+    assert any(k.startswith("layernorm") for k in names) == (not fused), names
+    plain = pkg.sparse_conv3d(f, w, b, m)
+    assert torch.equal(out, pkg.layer_norm(plain, g, be, eps=1e-6, silu=True))
+    out2 = pkg.sparse_conv3d(f, w, b, m, epilogue="ln_silu", eps=1e-5)
+    assert torch.equal(out2, pkg.layer_norm(plain, None, None, eps=1e-5, silu=True))
+    ref = oracle.layernorm(oracle.conv(f64, w64, b64, nbr), g64, be64, 1e-6, silu=True)
+    assert rel_err(out.float().cpu().numpy(), ref) <= 2e-2
+
+
 def _offset(t: torch.Tensor) -> torch.Tensor:
     """A contiguous copy of t whose data pointer is one element past a 256-byte boundary."""
     buf = torch.empty(t.numel() + 1, dtype=t.dtype, device=t.device)

@@ -356,6 +356,23 @@ int tsc_map_gather_plan(tsc_ctx* ctx, const int32_t* coords, const int32_t* nbr,
   return tsc::gather_plan_launch(ctx, coords, nbr, N, B, X, Y, Z, plan);
 }
 
+namespace {
+// The conv's epilogue for a requested TSC_EPI_BIAS_LN_SILU: inside the conv when its kernel owns
+// whole rows (conv_fuses_ln), else bias only, with the caller running the LayerNorm row pass.
+// Returns true when the caller still has to run that pass.
+bool set_ln_epilogue(ConvArgs& a, int32_t epilogue, const void* ln_gamma, const void* ln_beta,
+                     float eps) {
+  if (epilogue != TSC_EPI_BIAS_LN_SILU) return false;
+  a.ln_gamma = ln_gamma;
+  a.ln_beta = ln_beta;
+  a.ln_eps = eps;
+  a.epilogue = TSC_EPI_BIAS_LN_SILU;
+  if (conv_fuses_ln(a)) return false;
+  a.epilogue = TSC_EPI_BIAS;
+  return true;
+}
+}  // namespace
+
 int tsc_conv_planned(tsc_ctx* ctx, int32_t dtype, const void* feats, const void* weight,
                      const void* bias, const int32_t* nbr, const void* plan, int64_t N,
                      int32_t Ci, int32_t Co, int32_t epilogue, const void* residual,
@@ -377,8 +394,9 @@ int tsc_conv_planned(tsc_ctx* ctx, int32_t dtype, const void* feats, const void*
   ConvArgs a{dtype, feats, weight, bias, nbr, nullptr, N, Ci, Co,
              epilogue == TSC_EPI_BIAS_RESIDUAL ? TSC_EPI_BIAS_RESIDUAL : TSC_EPI_BIAS,
              residual, out, plan};
+  const bool ln_pass = set_ln_epilogue(a, epilogue, ln_gamma, ln_beta, eps);
   st = conv_launch(ctx, a);
-  if (st || epilogue != TSC_EPI_BIAS_LN_SILU) return st;
+  if (st || !ln_pass) return st;
   return layernorm_launch(ctx, dtype, out, N, Co, ln_gamma, ln_beta, eps, 1, out);
 }
 
@@ -405,8 +423,9 @@ int tsc_conv_fused(tsc_ctx* ctx, int32_t dtype, const void* feats, const void* w
   ConvArgs a{dtype, feats, weight, bias, nbr, order, N, Ci, Co,
              epilogue == TSC_EPI_BIAS_RESIDUAL ? TSC_EPI_BIAS_RESIDUAL : TSC_EPI_BIAS,
              residual, out};
+  const bool ln_pass = set_ln_epilogue(a, epilogue, ln_gamma, ln_beta, eps);
   st = conv_launch(ctx, a);
-  if (st || epilogue != TSC_EPI_BIAS_LN_SILU) return st;
+  if (st || !ln_pass) return st;
   return layernorm_launch(ctx, dtype, out, N, Co, ln_gamma, ln_beta, eps, 1, out);
 }
 
@@ -435,8 +454,9 @@ int tsc_conv_fused_noalloc(tsc_ctx* ctx, int32_t dtype, const void* feats, const
              residual, out};
   a.sched_scratch = ctx->sched_scratch;
   a.sched_scratch_bytes = kSchedScratchBytes;
+  const bool ln_pass = set_ln_epilogue(a, epilogue, ln_gamma, ln_beta, eps);
   st = conv_launch(ctx, a);
-  if (!st && epilogue == TSC_EPI_BIAS_LN_SILU)
+  if (!st && ln_pass)
     st = layernorm_launch(ctx, dtype, out, N, Co, ln_gamma, ln_beta, eps, 1, out);
   ctx->profile = prof;
   return st;
@@ -498,9 +518,10 @@ int tsc_resblock(tsc_ctx* ctx, int32_t dtype, const void* x, const int32_t* nbr,
   if (st) return st;
   // h = silu(LN(conv1(x) + b1));  out = x + conv2(h) + b2
   ConvArgs a1{dtype, x, w1, b1, nbr, order, N, C, C, TSC_EPI_BIAS, nullptr, h};
+  const bool ln_pass = set_ln_epilogue(a1, TSC_EPI_BIAS_LN_SILU, ln_gamma, ln_beta, eps);
   st = conv_launch(ctx, a1);
   if (st) return st;
-  st = layernorm_launch(ctx, dtype, h, N, C, ln_gamma, ln_beta, eps, 1, h);
+  if (ln_pass) st = layernorm_launch(ctx, dtype, h, N, C, ln_gamma, ln_beta, eps, 1, h);
   if (st) return st;
   ConvArgs a2{dtype, h, w2, b2, nbr, order, N, C, C, TSC_EPI_BIAS_RESIDUAL, x, out};
   return conv_launch(ctx, a2);

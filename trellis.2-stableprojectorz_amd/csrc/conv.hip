@@ -29,6 +29,7 @@
 #include <type_traits>
 #include <vector>
 
+#include "rownorm.h"
 #include "tsc_internal.h"
 
 namespace tsc {
@@ -309,7 +310,8 @@ __global__ void __launch_bounds__(64 * WM * WN)
                      const T* __restrict__ bias, const int32_t* __restrict__ nbr,
                      const int32_t* __restrict__ order, int64_t N, int32_t Ci, int32_t Co,
                      int32_t m_tiles, int32_t n_tiles, int32_t per_xcd,
-                     const int32_t* __restrict__ tile_map, const T* residual, T* out) {
+                     const int32_t* __restrict__ tile_map, const T* residual, T* out,
+                     const T* __restrict__ ln_g, const T* __restrict__ ln_b, float ln_eps) {
   using C = ConvCfg<T, BM, BN, KB, STAGES, WM, WN>;
   constexpr int SB = C::STAGE_BYTES;
   __shared__ __attribute__((aligned(16))) unsigned char ring_mem[STAGES * SB];
@@ -490,6 +492,11 @@ __global__ void __launch_bounds__(64 * WM * WN)
   __syncthreads();
   constexpr int EB = STAGES * SB;  // staging bytes
   constexpr bool RES = EPI == TSC_EPI_BIAS_RESIDUAL;
+  // LayerNorm + SiLU over whole rows (BN == Co): each staged row, rounded to T as the conv output
+  // would be stored, is normalized with the row pass's arithmetic (rowops.hip): lane l < BN/8
+  // sums its 8 consecutive columns in order, one wave butterfly per moment.
+  constexpr bool LN = EPI == TSC_EPI_BIAS_LN_SILU;
+  static_assert(!LN || (sizeof(T) == 2 && BN % 64 == 0 && BN <= 512), "LN epilogue shape");
   constexpr bool RES_IN_COPY = RES && (sizeof(T) == 4 || EB / (BN * 4) >= 32);
   using S = typename std::conditional<RES_IN_COPY, float, T>::type;  // staged element type
   constexpr int ROWB = BN * (int)sizeof(S);
@@ -525,6 +532,50 @@ __global__ void __launch_bounds__(64 * WM * WN)
       }
     }
     __syncthreads();
+    if constexpr (LN) {
+      constexpr int NV = BN / 8;  // 16-byte vectors per row
+      const bool has = lane < NV;
+      float g[8], bb[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        g[e] = (has && ln_g) ? to_f32<T>(ln_g[8 * lane + e]) : 1.f;
+        bb[e] = (has && ln_b) ? to_f32<T>(ln_b[8 * lane + e]) : 0.f;
+      }
+      for (int r = wid; r < RPP; r += C::NT / 64) {
+        const int32_t row = sRow[p0 + r];
+        if (row < 0) continue;  // wave-uniform
+        float v[8];
+        float s = 0.f;
+        if (has) {
+          const uint4 u = *(const uint4*)(sE + r * LDE + lane * 16);
+          const T* tv = (const T*)&u;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            v[e] = to_f32<T>(tv[e]);
+            s += v[e];
+          }
+        }
+        const float mean = rn_wave_sum(s) / (float)BN;
+        float qs = 0.f;
+        if (has) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float d = v[e] - mean;
+            qs += d * d;
+          }
+        }
+        const float var = rn_wave_sum(qs) / (float)BN;
+        const float inv = 1.0f / sqrtf(var + ln_eps);
+        if (has) {
+          T y[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) y[e] = from_f32<T>(rn_silu((v[e] - mean) * inv * g[e] + bb[e]));
+          *(uint4*)(out + (int64_t)row * Co + n0 + 8 * lane) = *(const uint4*)y;
+        }
+      }
+      __syncthreads();
+      continue;
+    }
     for (int q = tid; q < RPP * PIECES_PER_ROW; q += C::NT) {
       const int r = q / PIECES_PER_ROW, pc = q - r * PIECES_PER_ROW;
       const int32_t row = sRow[p0 + r];
@@ -791,11 +842,13 @@ int launch_cfg(tsc_ctx* ctx, const ConvArgs& a) {
   static const std::string name = std::string("conv_mfma_kernel<") +
       (sizeof(T) == 4 ? "f32" : std::is_same<T, __bf16>::value ? "bf16" : "f16") + "," +
       std::to_string(BM) + "x" + std::to_string(BN) + ",k" + std::to_string(KB) + ",s" +
-      std::to_string(STAGES) + (EPI == TSC_EPI_BIAS_RESIDUAL ? ",res>" : ">");
+      std::to_string(STAGES) +
+      (EPI == TSC_EPI_BIAS_RESIDUAL ? ",res>" : EPI == TSC_EPI_BIAS_LN_SILU ? ",ln>" : ">");
   ProfScope p(ctx, name.c_str());
   conv_mfma_kernel<T, BM, BN, KB, STAGES, WM, WN, EPI><<<grid, 64 * WM * WN, 0, ctx->stream>>>(
       (const T*)a.feats, (const T*)a.weight, (const T*)a.bias, a.nbr, a.order, a.N, a.Ci, a.Co,
-      m_tiles, n_tiles, per_xcd, tile_map, (const T*)a.residual, (T*)a.out);
+      m_tiles, n_tiles, per_xcd, tile_map, (const T*)a.residual, (T*)a.out,
+      (const T*)a.ln_gamma, (const T*)a.ln_beta, a.ln_eps);
   return check_hip(hipGetLastError(), "conv launch");
 }
 
@@ -1317,8 +1370,26 @@ int dispatch_tiles(tsc_ctx* ctx, const ConvArgs& a) {
   return launch_cfg<T, 128, 32, 32, 4, 1, EPI>(ctx, a);
 }
 
+// The ring configurations of dispatch_tiles whose column tile is the whole row (BN == Co), with
+// the LayerNorm + SiLU epilogue; conv_fuses_ln admits exactly these shapes.
+template <typename T>
+int dispatch_ln(tsc_ctx* ctx, const ConvArgs& a) {
+  if constexpr (sizeof(T) == 2) {
+    const int kb = pick_kb(a.Ci * 2);
+    if (a.Co == 256 && kb >= 64)
+      return launch_cfg<T, 256, 256, 64, 2, 4, TSC_EPI_BIAS_LN_SILU, 1>(ctx, a);
+    if (a.Co == 128 && kb >= 64) return launch_cfg<T, 128, 128, 64, 2, 2, TSC_EPI_BIAS_LN_SILU>(ctx, a);
+    if (a.Co == 64) {
+      if (kb >= 64) return launch_cfg<T, 128, 64, 64, 4, 1, TSC_EPI_BIAS_LN_SILU>(ctx, a);
+      return launch_cfg<T, 128, 64, 32, 4, 1, TSC_EPI_BIAS_LN_SILU>(ctx, a);
+    }
+  }
+  return fail(TSC_ERR_INVALID, "conv: no fused LayerNorm epilogue for Ci=%d Co=%d", a.Ci, a.Co);
+}
+
 template <typename T>
 int dispatch_epi(tsc_ctx* ctx, const ConvArgs& a, bool tuned) {
+  if (a.epilogue == TSC_EPI_BIAS_LN_SILU) return dispatch_ln<T>(ctx, a);
   if (a.epilogue == TSC_EPI_BIAS_RESIDUAL)
     return tuned ? dispatch_tiles<T, TSC_EPI_BIAS_RESIDUAL>(ctx, a)
                  : dispatch_generic<T, TSC_EPI_BIAS_RESIDUAL>(ctx, a);
@@ -1335,6 +1406,20 @@ bool conv_tuned_shape(const ConvArgs& a) {
   return (a.Ci * es) % 32 == 0 && a.Co % 32 == 0 && al16(a.feats) && al16(a.weight) &&
          al16(a.out) && (!a.bias || al16(a.bias)) &&
          (a.epilogue != TSC_EPI_BIAS_RESIDUAL || al16(a.residual));
+}
+
+bool conv_fuses_ln(const ConvArgs& a) {
+  if (a.dtype == TSC_F32 || a.plan) return false;
+  ConvArgs b = a;
+  b.epilogue = TSC_EPI_BIAS;
+  auto al16 = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
+  if (!conv_tuned_shape(b) || conv_gather_supported(b)) return false;
+  if ((a.ln_gamma && !al16(a.ln_gamma)) || (a.ln_beta && !al16(a.ln_beta))) return false;
+  // The ring path of dispatch_tiles (rows wider than 64 bytes, not the narrow kernels) with a
+  // column tile equal to Co.
+  if (a.Ci * 2 <= 64) return false;
+  const int kb = pick_kb(a.Ci * 2);
+  return (a.Co == 256 && kb >= 64) || (a.Co == 128 && kb >= 64) || a.Co == 64;
 }
 
 int conv_launch(tsc_ctx* ctx, const ConvArgs& a) {

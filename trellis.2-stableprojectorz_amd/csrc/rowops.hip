@@ -11,6 +11,7 @@
 // mean and variance come from two wave reductions over those registers, and the normalised row
 // is written once.  Longer or unaligned rows take a three-pass strided kernel.
 
+#include "rownorm.h"
 #include "tsc_internal.h"
 
 namespace tsc {
@@ -46,13 +47,8 @@ __device__ __forceinline__ uint4 pack(const float* f) {
   return u;
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
-
-__device__ __forceinline__ float silu_f(float x) { return x * (1.0f / (1.0f + __expf(-x))); }
+__device__ __forceinline__ float wave_sum(float v) { return rn_wave_sum(v); }
+__device__ __forceinline__ float silu_f(float x) { return rn_silu(x); }
 
 // MAXV = max 16-byte vectors per lane (row length <= 64 * MAXV * Vec<T>::n).
 typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));

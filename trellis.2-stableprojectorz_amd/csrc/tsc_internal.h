@@ -119,7 +119,8 @@ struct ConvArgs {
   const int32_t* order;  // may be null
   int64_t N;
   int32_t Ci, Co;
-  int32_t epilogue;      // TSC_EPI_BIAS or TSC_EPI_BIAS_RESIDUAL (LN handled by the caller)
+  int32_t epilogue;      // TSC_EPI_BIAS, TSC_EPI_BIAS_RESIDUAL, or TSC_EPI_BIAS_LN_SILU when
+                         // conv_fuses_ln (else LN runs as a row pass by the caller)
   const void* residual;  // for TSC_EPI_BIAS_RESIDUAL
   void* out;
   const void* plan = nullptr;  // gather plan (conv_gather.hip) or null
@@ -127,6 +128,11 @@ struct ConvArgs {
   // (tsc_conv_fused_noalloc), and its size in bytes.
   void* sched_scratch = nullptr;
   size_t sched_scratch_bytes = 0;
+  // LayerNorm + SiLU inside the conv epilogue (epilogue TSC_EPI_BIAS_LN_SILU, only where
+  // conv_fuses_ln says so): gamma / beta (Co, NULL = 1 / 0) and eps.
+  const void* ln_gamma = nullptr;
+  const void* ln_beta = nullptr;
+  float ln_eps = 0.f;
 };
 // Row tiles the longest-first schedule handles (beyond it tiles run in row order), and the
 // schedule's largest scratch: a cost per tile plus 8 lists of ceil(tiles / 8) slots.
@@ -140,6 +146,10 @@ int sched_scratch_ptr(int device, void** out);
 int conv_launch(tsc_ctx* ctx, const ConvArgs& a);
 // True when the tuned kernels take this shape and these buffers (else the generic kernel runs).
 bool conv_tuned_shape(const ConvArgs& a);
+// True when the kernel conv_launch picks for `a` owns whole output rows and can apply
+// LayerNorm + SiLU in its epilogue (16-bit wide rows with Co of 64, 128 or 256, 16-byte aligned
+// gamma / beta); callers then pass epilogue TSC_EPI_BIAS_LN_SILU instead of a row pass.
+bool conv_fuses_ln(const ConvArgs& a);
 
 // ---- gather plan + planned narrow conv (conv_gather.hip) ----
 constexpr int kPlanRows = 64;                   // rows per plan tile

@@ -31,7 +31,8 @@ _DEMANGLED_TYPES = {"__bf16": "bf16", "_Float16": "f16", "float": "f32"}
 def _conv_name(kind: str, t: str, nums: list) -> str:
     if kind == "conv_mfma_kernel":  # BM, BN, KB, STAGES, WM, WN, EPI
         bm, bn, kb, st, _, _, epi = nums
-        return f"conv_mfma_kernel<{t},{bm}x{bn},k{kb},s{st}{',res' if epi == '1' else ''}>"
+        tag = {"1": ",res", "2": ",ln"}.get(epi, "")
+        return f"conv_mfma_kernel<{t},{bm}x{bn},k{kb},s{st}{tag}>"
     if kind == "conv_gather_kernel":  # EPI
         return f"conv_gather_kernel<{t}{',res' if nums[0] == '1' else ''}>"
     if kind == "conv_narrow_kernel":  # CO, EPI, threads
