@@ -233,7 +233,7 @@ __global__ void __launch_bounds__(kOrdThreads)
 // Thread t owns entries [t*E, t*E + E) in registers throughout the tile loop, so a pass over the
 // entries is register work plus two block reductions.
 constexpr int kGrChunk = 4096;   // rows per chunk (and at most this many entries)
-constexpr int kGrThreads = 1024;
+constexpr int kGrThreads = 512;
 constexpr int kGrTile = 256;     // rows per tile of the 256-row conv kernels
 constexpr int kGrPerThread = kGrChunk / kGrThreads;  // rows, and entries at most, per thread
 static_assert(kOrdTilesPerWin * kOrdTile % kGrChunk == 0, "chunks never straddle a window");
