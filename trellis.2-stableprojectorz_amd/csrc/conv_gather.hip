@@ -218,8 +218,6 @@ __device__ __forceinline__ void mfma16<__bf16>(const uint4& a, const uint4& b, f
                                                 __builtin_bit_cast(bf16x8_t, b), acc, 0, 0, 0);
 }
 
-__device__ __attribute__((aligned(16))) uint4 g_zero_row[4];
-
 constexpr int kGWaves = 7;    // waves per block (one block per CU: LDS-bound)
 constexpr int kGStage = 208;  // LDS row slots per wave (slot 0 = zeros); tiles need d < 208
 constexpr int kGChunks = kGStage / 16;
@@ -281,68 +279,66 @@ __global__ void __launch_bounds__(64 * kGWaves)
   const int first = __builtin_amdgcn_readfirstlane(t_begin + slot_in_half * kGWaves + wid);
   if (first >= t_end) return;
 
-  auto count_of = [&](int t) {
-    const int d = __builtin_amdgcn_readfirstlane(pcount[t]);
-    return d < kGStage ? d : -1;  // -1: not staged
+  // Prefetch of a tile is straight-line code: per-lane loads whose addresses are clamped (never
+  // skipped), so the compiler can count them exactly.  Loads under per-chunk branches made it
+  // wait for every outstanding load before each dependent one (one vmcnt counts all loads in
+  // order), which serialised a tile's ~20 index and row loads into one round trip each.
+  //   meta  one load: lanes 0-3 the tile's four 16-row tap masks, lane 4 its distinct-row count
+  //   idx   the list entries of slots 16c + j (always inside the tile's kPlanSlots entries)
+  //   rows  row idx[c] piece p for slots below the count, else row 0 (valid, never staged)
+  auto load_meta = [&](int t) {
+    return lane < 4 ? (int32_t)prbm[t * 4 + lane] : pcount[t];
   };
-  auto load_masks = [&](int t, uint32_t (&m)[4]) {
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb) m[rb] = __builtin_amdgcn_readfirstlane(prbm[t * 4 + rb]);
-  };
-  auto load_tbl = [&](int t, uint4& ta, uint4& tb2) {
-    const uint4* tq = pslots + (int64_t)t * kTableQ;
-    ta = tq[lane];
-    if (lane < kTableQ - 64) tb2 = tq[64 + lane];
+  auto meta_count = [&](int32_t meta) {
+    const int dd = __builtin_amdgcn_readlane(meta, 4);
+    return dd < kGStage ? dd : -1;  // -1: not staged
   };
   typedef uint32_t xvec_t __attribute__((ext_vector_type(4 * kGChunks)));
-  int32_t idx[kGChunks] = {};
+  int32_t idx[kGChunks];
   xvec_t x = {};
   auto chunk_mask = [](int d) {
     return d > 0 ? __builtin_amdgcn_readfirstlane((1u << ((d + 15) >> 4)) - 1u) : 0u;
   };
-  auto load_idx = [&](int t, int d) {
-    const uint32_t cm = chunk_mask(d);
+  auto load_idx = [&](int t) {
     const int32_t* list = plist + (int64_t)t * kPlanSlots;
 #pragma unroll
-    for (int c = 0; c < kGChunks; ++c)
-      if ((cm >> c) & 1u) {
-        const int i = 16 * c + j;
-        idx[c] = i < d ? list[i] : -1;
-      }
+    for (int c = 0; c < kGChunks; ++c) idx[c] = list[16 * c + j];
   };
   auto gather = [&](int d) {
-    const uint32_t cm = chunk_mask(d);
 #pragma unroll
-    for (int c = 0; c < kGChunks; ++c)
-      if ((cm >> c) & 1u) {
-        const int32_t r = idx[c];
-        const uint4* src = (r >= 0 && r < N) ? (const uint4*)(feats + (int64_t)r * 32) + p
-                                             : g_zero_row + p;
-        const uint4 vv = *src;
-        x[4 * c] = vv.x;
-        x[4 * c + 1] = vv.y;
-        x[4 * c + 2] = vv.z;
-        x[4 * c + 3] = vv.w;
-      }
+    for (int c = 0; c < kGChunks; ++c) {
+      const int32_t r = idx[c];
+      const bool ok = 16 * c + j < d && r >= 0 && r < N;
+      const uint4 vv = ((const uint4*)(feats + (int64_t)(ok ? r : 0) * 32))[p];
+      x[4 * c] = vv.x;
+      x[4 * c + 1] = vv.y;
+      x[4 * c + 2] = vv.z;
+      x[4 * c + 3] = vv.w;
+    }
+  };
+  auto load_tbl = [&](int t, uint4& ta, uint4& tb2) {
+    const uint4* tq = pslots + (int64_t)t * kTableQ;
+    ta = tq[lane];
+    tb2 = tq[64 + (lane < kTableQ - 64 ? lane : 0)];
   };
 
-  // Prologue: the first tile's rows gathered and its table loaded; the next tile's indices.
+  // Prologue: the first tile's rows gathered and its table loaded; the next tile's metadata and
+  // indices.  A missing next tile repeats the current one (its loads stay in bounds, unused).
   int cur = first;
-  int d = count_of(cur);
+  int32_t meta = load_meta(cur);
+  load_idx(cur);
+  int d = meta_count(meta);
   uint32_t m[4];
-  load_masks(cur, m);
-  load_idx(cur, d);
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb) m[rb] = (uint32_t)__builtin_amdgcn_readlane(meta, rb);
   gather(d);
   uint4 ta, tb2;
   load_tbl(cur, ta, tb2);
+  int32_t row_n = prow[(int64_t)cur * kPlanRows + lane];
   int next = __builtin_amdgcn_readfirstlane(cur + stride);
-  int dn = -1;
-  uint32_t mn[4] = {0u, 0u, 0u, 0u};
-  if (next < t_end) {
-    dn = count_of(next);
-    load_masks(next, mn);
-    load_idx(next, dn);
-  }
+  int nx = next < t_end ? next : cur;
+  int32_t meta_n = load_meta(nx);
+  load_idx(nx);
 
   for (;;) {
     // Stage tile `cur`: rows and slot table into the wave's LDS.
@@ -363,24 +359,20 @@ __global__ void __launch_bounds__(64 * kGWaves)
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     const uint32_t mc[4] = {m[0], m[1], m[2], m[3]};
     const bool staged = d >= 0;
-    int32_t row_c = prow[(int64_t)cur * kPlanRows + lane];
-    row_c = row_c < N ? row_c : -1;
-    // Tile `next`: rows and table go out now; the tile after it gets its head and indices.
+    int32_t row_c = row_n < N ? row_n : -1;
+    // Tile `next` (or `cur` again at the end): rows, table and row list go out now; the tile
+    // after it gets its metadata and indices.
     const bool has_next = next < t_end;
-    if (has_next) {
-      gather(dn);
-      load_tbl(next, ta, tb2);
-      d = dn;
+    d = meta_count(meta_n);
 #pragma unroll
-      for (int rb = 0; rb < 4; ++rb) m[rb] = mn[rb];
-      const int nn = __builtin_amdgcn_readfirstlane(next + stride);
-      if (nn < t_end) {
-        dn = count_of(nn);
-        load_masks(nn, mn);
-        load_idx(nn, dn);
-      }
-    }
-
+    for (int rb = 0; rb < 4; ++rb) m[rb] = (uint32_t)__builtin_amdgcn_readlane(meta_n, rb);
+    gather(d);
+    load_tbl(nx, ta, tb2);
+    row_n = prow[(int64_t)nx * kPlanRows + lane];
+    const int nn = __builtin_amdgcn_readfirstlane(next + stride);
+    const int nnx = nn < t_end ? nn : nx;
+    meta_n = load_meta(nnx);
+    load_idx(nnx);
     f32x4_t acc[4][2];
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb)
@@ -440,7 +432,9 @@ __global__ void __launch_bounds__(64 * kGWaves)
         for (int rb = 0; rb < 4; ++rb) {
           const int32_t r = __shfl(row_c, rb * 16 + l16, 64);
           const int32_t e = r >= 0 ? nbr[(int64_t)r * kTaps + v] : -1;
-          b[rb] = (e >= 0 && e < N) ? ((const uint4*)(feats + (int64_t)e * 32))[q] : g_zero_row[q];
+          const bool ok = e >= 0 && e < N;
+          const uint4 bv4 = ((const uint4*)(feats + (int64_t)(ok ? e : 0) * 32))[q];
+          b[rb] = ok ? bv4 : make_uint4(0u, 0u, 0u, 0u);
         }
         mm(b, a);
       }
@@ -473,7 +467,8 @@ __global__ void __launch_bounds__(64 * kGWaves)
     }
     if (!has_next) break;
     cur = next;
-    next = __builtin_amdgcn_readfirstlane(next + stride);
+    next = nn;
+    nx = nnx;
   }
 }
 
