@@ -11,7 +11,8 @@
 // sequence allows, so a tile's union of taps stays close to one row's.  Ties keep key order.
 //
 // Stable LSD radix sort, three passes of <= 9 bits, over tiles of 16384 rows (16 per window):
-//   mask     key = mask of row perm[i], val = perm[i]; tile histogram of digit 0
+//   rowmask  per row, reading the map in row order: the Gray rank of its mask
+//   mask     key = rowmask[perm[i]], val = perm[i]; tile histogram of digit 0
 //   scan     per window: digit-major, tile-minor exclusive offsets of the 16 tiles' counts
 //   scatter  per tile: wave-ballot stable ranks (one ballot per digit bit -> peer mask; popcount
 //            of lower peers + the wave's running count; per-digit offsets across waves), written
@@ -68,8 +69,47 @@ __device__ __forceinline__ int digit(uint32_t k, int shift) {
   return (int)((k >> shift) & (uint32_t)(kOrdBins - 1));
 }
 
+// Row masks in row order: each block copies the neighbor rows of 256 consecutive rows into LDS with
+// coalesced loads (27 dwords per thread), then thread t forms row r0 + t's 26-bit mask and ranks
+// it in the reflected binary (Gray) sequence, whose neighbors differ in one tap where numeric
+// neighbors can differ in many low taps.  Reading the map in row order is ~2.5x faster than
+// reading its 108-byte rows in key order (random addresses, two cache lines each).
+constexpr int kRowThreads = 256;
+__global__ void __launch_bounds__(kRowThreads)
+    ord_rowmask_kernel(const int32_t* __restrict__ nbr, int64_t n, uint32_t* __restrict__ rowmask) {
+  __shared__ int32_t s[kRowThreads * 27];
+  const int tid = threadIdx.x;
+  const int64_t r0 = (int64_t)blockIdx.x * kRowThreads;
+  const int rows = (int)(n - r0 < kRowThreads ? n - r0 : kRowThreads);
+  const int32_t* src = nbr + r0 * 27;
+  if (rows == kRowThreads) {
+    int32_t v[27];
+#pragma unroll
+    for (int k = 0; k < 27; ++k) v[k] = src[k * kRowThreads + tid];
+#pragma unroll
+    for (int k = 0; k < 27; ++k) s[k * kRowThreads + tid] = v[k];
+  } else {
+    for (int w = tid; w < rows * 27; w += kRowThreads) s[w] = src[w];
+  }
+  __syncthreads();
+  if (tid < rows) {
+    const int32_t* nr = s + tid * 27;  // stride 27 words: conflict-free
+    uint32_t m = 0;
+#pragma unroll
+    for (int k = 0; k < kOrdMaskBits; ++k) m = (m << 1) | (uint32_t)(nr[kMaskTap[k]] >= 0);
+    m ^= m >> 1;
+    m ^= m >> 2;
+    m ^= m >> 4;
+    m ^= m >> 8;
+    m ^= m >> 16;
+    rowmask[r0 + tid] = m;
+  }
+}
+
+// Keys of the first sort pass: key = rank of row perm[i]'s mask, val = perm[i]; tile histogram of
+// digit 0.
 __global__ void __launch_bounds__(kOrdThreads)
-    ord_mask_kernel(const int32_t* __restrict__ nbr, const int32_t* __restrict__ perm,
+    ord_mask_kernel(const uint32_t* __restrict__ rowmask, const int32_t* __restrict__ perm,
                     int64_t n, uint32_t* __restrict__ keys, int32_t* __restrict__ vals,
                     int* __restrict__ counts) {
   __shared__ int hist[kOrdBins];
@@ -77,25 +117,30 @@ __global__ void __launch_bounds__(kOrdThreads)
   for (int d = tid; d < kOrdBins; d += kOrdThreads) hist[d] = 0;
   __syncthreads();
   const int64_t t0 = (int64_t)blockIdx.x * kOrdTile;
-#pragma unroll 4
-  for (int j = 0; j < kOrdItems; ++j) {
-    const int64_t i = t0 + j * kOrdThreads + tid;
-    if (i < n) {
-      const int32_t r = perm ? perm[i] : (int32_t)i;
-      const int32_t* nr = nbr + (int64_t)r * 27;
-      uint32_t m = 0;
+  if (t0 + kOrdTile <= n) {
+    int32_t r[kOrdItems];
 #pragma unroll
-      for (int k = 0; k < kOrdMaskBits; ++k) m = (m << 1) | (uint32_t)(nr[kMaskTap[k]] >= 0);
-      // Sort by the mask's position in the reflected binary (Gray) sequence: neighbors in that
-      // sequence differ in one tap, where numeric neighbors can differ in many low taps.
-      m ^= m >> 1;
-      m ^= m >> 2;
-      m ^= m >> 4;
-      m ^= m >> 8;
-      m ^= m >> 16;
-      keys[i] = m;
-      vals[i] = r;
-      atomicAdd(&hist[digit(m, 0)], 1);
+    for (int j = 0; j < kOrdItems; ++j) r[j] = perm ? perm[t0 + j * kOrdThreads + tid] : (int32_t)(t0 + j * kOrdThreads + tid);
+    uint32_t m[kOrdItems];
+#pragma unroll
+    for (int j = 0; j < kOrdItems; ++j) m[j] = rowmask[r[j]];
+#pragma unroll
+    for (int j = 0; j < kOrdItems; ++j) {
+      const int64_t i = t0 + j * kOrdThreads + tid;
+      keys[i] = m[j];
+      vals[i] = r[j];
+      atomicAdd(&hist[digit(m[j], 0)], 1);
+    }
+  } else {
+    for (int j = 0; j < kOrdItems; ++j) {
+      const int64_t i = t0 + j * kOrdThreads + tid;
+      if (i < n) {
+        const int32_t r = perm ? perm[i] : (int32_t)i;
+        const uint32_t m = rowmask[r];
+        keys[i] = m;
+        vals[i] = r;
+        atomicAdd(&hist[digit(m, 0)], 1);
+      }
     }
   }
   __syncthreads();
@@ -480,7 +525,8 @@ int conv_order_launch(tsc_ctx* ctx, const int32_t* nbr, const int32_t* perm, int
   const int ntiles = (int)((N + kOrdTile - 1) / kOrdTile);
   const int nwin = (ntiles + kOrdTilesPerWin - 1) / kOrdTilesPerWin;
   const size_t need = 2 * align_up((size_t)N * 4, 256) + 2 * align_up((size_t)N * 4, 256) +
-                      2 * align_up((size_t)ntiles * kOrdBins * 4, 256);
+                      2 * align_up((size_t)ntiles * kOrdBins * 4, 256) +
+                      align_up((size_t)N * 4, 256);
   void* ws;
   int st = workspace(ctx, need, &ws);
   if (st) return st;
@@ -491,9 +537,12 @@ int conv_order_launch(tsc_ctx* ctx, const int32_t* nbr, const int32_t* perm, int
   int32_t* vB = cv.take<int32_t>(N);
   int* counts = cv.take<int>((int64_t)ntiles * kOrdBins);
   int* offs = cv.take<int>((int64_t)ntiles * kOrdBins);
+  uint32_t* rowmask = cv.take<uint32_t>(N);
   hipStream_t s = ctx->stream;
   ProfScope p(ctx, "conv_order");
-  ord_mask_kernel<<<ntiles, kOrdThreads, 0, s>>>(nbr, perm, N, kA, vA, counts);
+  ord_rowmask_kernel<<<(unsigned)((N + kRowThreads - 1) / kRowThreads), kRowThreads, 0, s>>>(
+      nbr, N, rowmask);
+  ord_mask_kernel<<<ntiles, kOrdThreads, 0, s>>>(rowmask, perm, N, kA, vA, counts);
   uint32_t *kc = kA, *kn = kB;
   int32_t *vc = vA, *vn = vB;
   for (int pass = 0; pass < kOrdPasses; ++pass) {
