@@ -110,10 +110,13 @@ int tsc_map_build(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t B, int
                   void* keys_out, int32_t* perm_out, int32_t* nbr_out, uint32_t* status_dev);
 
 /* Row order for tsc_conv / tsc_conv_fused / tsc_resblock: the map's sorted rows (perm, from
- * tsc_map_build; NULL = 0..N-1) regrouped inside windows of 262144 consecutive entries so that rows
- * * with the same set of present neighbors are contiguous.  The conv kernels skip a tap for a tile
- * of rows only when no row of the tile has that neighbor, so grouped rows skip far more absent
- * (zero) neighbor work than key order does on thin shells.  order_out: device int32 (N).
+ * tsc_map_build; NULL = 0..N-1), sorted inside windows of 262144 consecutive entries by the
+ * reflected-binary rank of their 26-bit mask of present neighbors (ties keep the given order),
+ * then regrouped inside chunks of 4096 into 256-row tiles of masks contained in a small tap set.
+ * The conv kernels skip a tap for a tile of rows only when no row of the tile has that neighbor,
+ * so grouped rows skip far more absent (zero) neighbor work than key order does on thin shells.
+ * order_out: device int32 (N), a permutation of 0..N-1.  Stream-ordered; uses the context's
+ * workspace.
  * No counterpart in the reference: an acceleration structure derived from the neighbor map,
  * meant to be cached beside it (the reference caches the map per tensor, conv3d.ts:144-148). */
 int tsc_map_conv_order(tsc_ctx* ctx, const int32_t* nbr, const int32_t* perm, int64_t N,

@@ -154,21 +154,9 @@ def test_conv_order_invariance_bit_exact(pkg, dev, dtype):
     assert torch.equal(ident, keyorder)
 
 
-@pytest.mark.parametrize("workload", ["map512", "wide128_bf16", "conv64_f32"])
-def test_map_conv_order(pkg, dev, workload):
-    """The conv order: inside each window of 262144 consecutive key-sorted rows, rows sorted by the
-    Gray-sequence rank of their 26-bit mask of present neighbors (corner taps in the top bits, then
-    edges, then faces, each class in tap order; tap 13 left out), ties in key order; then inside
-    each chunk of 4096 sorted rows, 256-row tiles regrouped greedily (_greedy_tiles).  Exact
-    match, and the regrouping never raises the taps the 256-row tiles process."""
-    coords = pkg.workloads.make_coords(workload)
-    batch = int(coords[:, 0].max()) + 1
-    m = _map(pkg, dev, coords, batch, pkg.workloads.grid_shape(workload))
-    print(f"  conv order {workload} N={len(coords)}", flush=True)
-    order = m.conv_order().cpu().numpy()
-    perm = m.perm.cpu().numpy()
-    n = len(coords)
-    present = m.nbr.cpu().numpy() >= 0
+def _order_model(present, perm):
+    """CPU model of tsc_map_conv_order: (order, Gray rank of every row's mask, sorted order)."""
+    n = len(present)
     # taps by the number of offset coordinates that are not 0 (3 = corner, 2 = edge, 1 = face)
     cls = [sum(c != 1 for c in (v // 9, v // 3 % 3, v % 3)) for v in range(27)]
     taps = sorted((v for v in range(27) if v != 13), key=lambda v: (-cls[v], v))
@@ -182,18 +170,51 @@ def test_map_conv_order(pkg, dev, workload):
     for i in range(26):
         rank |= (np.bitwise_xor.reduce([(m26 >> j) & 1 for j in range(i, 26)], axis=0)) << i
     assert rank[m26 == 0].max(initial=0) == 0
-    m26 = rank
     srt = np.empty(n, np.int64)
     win = 262144
     for w0 in range(0, n, win):
         rows = perm[w0:w0 + win]
-        srt[w0:w0 + win] = rows[np.argsort(m26[rows], kind="stable")]
-    want = _greedy_tiles(srt, m26[srt])
+        srt[w0:w0 + win] = rows[np.argsort(rank[rows], kind="stable")]
+    return _greedy_tiles(srt, rank[srt]), rank, srt
+
+
+@pytest.mark.parametrize("workload", ["map512", "wide128_bf16", "conv64_f32"])
+def test_map_conv_order(pkg, dev, workload):
+    """The conv order: inside each window of 262144 consecutive key-sorted rows, rows sorted by the
+    Gray-sequence rank of their 26-bit mask of present neighbors (corner taps in the top bits, then
+    edges, then faces, each class in tap order; tap 13 left out), ties in key order; then inside
+    each chunk of 4096 sorted rows, 256-row tiles regrouped greedily (_greedy_tiles).  Exact
+    match, and the regrouping never raises the taps the 256-row tiles process."""
+    coords = pkg.workloads.make_coords(workload)
+    batch = int(coords[:, 0].max()) + 1
+    m = _map(pkg, dev, coords, batch, pkg.workloads.grid_shape(workload))
+    print(f"  conv order {workload} N={len(coords)}", flush=True)
+    order = m.conv_order().cpu().numpy()
+    n = len(coords)
+    want, rank, srt = _order_model(m.nbr.cpu().numpy() >= 0, m.perm.cpu().numpy())
     np.testing.assert_array_equal(order, want)
     assert np.array_equal(np.sort(order), np.arange(n))
-    mask = (m26 ^ (m26 >> 1))[order], (m26 ^ (m26 >> 1))[srt]  # neighbor masks (ranks -> codes)
+    mask = (rank ^ (rank >> 1))[order], (rank ^ (rank >> 1))[srt]  # neighbor masks (ranks -> codes)
     taps = [_tile_taps(x, 256) for x in mask]
     assert taps[0] <= taps[1], taps
+
+
+@pytest.mark.parametrize("rows", [200, None])
+def test_map_conv_order_without_perm(pkg, dev, rows):
+    """perm = NULL orders rows 0..N-1 as given (the same as passing the identity), on ragged
+    sizes: a 200-row map (every kernel's only block partial) and the conv64 set (25 k rows, no
+    multiple of the 256-, 4096- or 16384-row tiles)."""
+    coords = pkg.workloads.make_coords("conv64_f32")
+    if rows is not None:
+        coords = coords[:rows]
+    m = _map(pkg, dev, coords, 1, pkg.workloads.grid_shape("conv64_f32"))
+    n = len(coords)
+    print(f"  conv order without perm N={n}", flush=True)
+    got = pkg.map_conv_order(m.nbr, None).cpu().numpy()
+    ident = torch.arange(n, dtype=torch.int32, device=dev)
+    np.testing.assert_array_equal(got, pkg.map_conv_order(m.nbr, ident).cpu().numpy())
+    want, _, _ = _order_model(m.nbr.cpu().numpy() >= 0, np.arange(n))
+    np.testing.assert_array_equal(got, want)
 
 
 def _popcount(a):
