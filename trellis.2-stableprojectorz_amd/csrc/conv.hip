@@ -756,11 +756,26 @@ __global__ void __launch_bounds__(64 * WM * WN)
     if (c + 1 < nchunks) store_chunk(buf ^ 1);
   }
 
-  // Epilogue: bias (+ residual), round to T, scatter rows back to their original positions.
+  // Epilogue: bias (+ residual), round to T, scatter rows back to their original positions.  The
+  // residual values are all loaded before the first store (rows past N read row 0 and are not
+  // stored): loads under per-row branches would each wait for the one before.  Every output
+  // element is read and written by the same lane, so the output may alias the residual.
 #pragma unroll
   for (int j = 0; j < C::FN; ++j) {
     const int co = n0 + wn * C::WTN + j * 32 + (lane & 31);
     const float bv = bias ? to_f32<T>(bias[co]) : 0.f;
+    float rv[C::FM][16];
+#pragma unroll
+    for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        rv[i][e] = 0.f;
+        if (EPI == TSC_EPI_BIAS_RESIDUAL) {
+          const int rl = wm * C::WTM + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+          const int32_t row = sRow[rl];
+          rv[i][e] = to_f32<T>(residual[(int64_t)(row >= 0 ? row : 0) * Co + co]);
+        }
+      }
 #pragma unroll
     for (int i = 0; i < C::FM; ++i) {
 #pragma unroll
@@ -769,9 +784,8 @@ __global__ void __launch_bounds__(64 * WM * WN)
         const int32_t row = sRow[rl];
         if (row >= 0) {
           float val = acc[i][j][e] + bv;
-          const int64_t o = (int64_t)row * Co + co;
-          if (EPI == TSC_EPI_BIAS_RESIDUAL) val += to_f32<T>(residual[o]);
-          out[o] = from_f32<T>(val);
+          if (EPI == TSC_EPI_BIAS_RESIDUAL) val += rv[i][e];
+          out[(int64_t)row * Co + co] = from_f32<T>(val);
         }
       }
     }
@@ -1068,10 +1082,30 @@ __global__ void __launch_bounds__(NT)
       }
     }
 
-    // Epilogue.
+    // Epilogue.  Bias and residual values are all loaded before the first store (rows past N
+    // read row 0 and are not stored): loads under the per-row branches would each wait for the
+    // one before.  Each output element is read and written by the same lane, so the output may
+    // alias the residual.
+    struct alignas(4 * sizeof(T)) V4 {
+      T v[4];
+    };
+    int32_t rows[2];
+    V4 bt[CB], rt[2][CB];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) rows[rb] = __shfl(my_row, rb * 16 + l16, 64);
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+      const int c0 = cb * 16 + 4 * q;
+      if (bias) bt[cb] = *(const V4*)(bias + c0);
+      if (EPI == TSC_EPI_BIAS_RESIDUAL) {
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+          rt[rb][cb] = *(const V4*)(residual + (int64_t)(rows[rb] >= 0 ? rows[rb] : 0) * CO + c0);
+      }
+    }
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
-      const int32_t row = __shfl(my_row, rb * 16 + l16, 64);
+      const int32_t row = rows[rb];
       if (row < 0) continue;
 #pragma unroll
       for (int cb = 0; cb < CB; ++cb) {
@@ -1079,18 +1113,13 @@ __global__ void __launch_bounds__(NT)
         float x[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) x[i] = acc[rb][cb][i];
-        struct alignas(4 * sizeof(T)) V4 {
-          T v[4];
-        };
         if (bias) {
-          const V4 bt = *(const V4*)(bias + c0);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) x[i] += to_f32<T>(bt.v[i]);
+          for (int i = 0; i < 4; ++i) x[i] += to_f32<T>(bt[cb].v[i]);
         }
         if (EPI == TSC_EPI_BIAS_RESIDUAL) {
-          const V4 rt = *(const V4*)(residual + (int64_t)row * CO + c0);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) x[i] += to_f32<T>(rt.v[i]);
+          for (int i = 0; i < 4; ++i) x[i] += to_f32<T>(rt[rb][cb].v[i]);
         }
         V4 y;
 #pragma unroll
@@ -1271,15 +1300,24 @@ __global__ void __launch_bounds__(kGenThreads)
   const int co = n0 + wn * 32 + (lane & 31);
   if (co >= Co) return;
   const float bv = bias ? to_f32<T>(bias[co]) : 0.f;
+  // Residual values first, all loads before the first store (see conv_regstage_kernel).
+  float rv[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    rv[e] = 0.f;
+    if (EPI == TSC_EPI_BIAS_RESIDUAL) {
+      const int32_t row = sRow[wm * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3)];
+      rv[e] = to_f32<T>(residual[(int64_t)(row >= 0 ? row : 0) * Co + co]);
+    }
+  }
 #pragma unroll
   for (int e = 0; e < 16; ++e) {
     const int rl = wm * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
     const int32_t row = sRow[rl];
     if (row < 0) continue;
-    const int64_t o = (int64_t)row * Co + co;
     float val = acc[e] + bv;
-    if (EPI == TSC_EPI_BIAS_RESIDUAL) val += to_f32<T>(residual[o]);
-    out[o] = from_f32<T>(val);
+    if (EPI == TSC_EPI_BIAS_RESIDUAL) val += rv[e];
+    out[(int64_t)row * Co + co] = from_f32<T>(val);
   }
 }
 
