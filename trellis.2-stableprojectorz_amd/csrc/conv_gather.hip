@@ -440,10 +440,27 @@ __global__ void __launch_bounds__(64 * kGWaves)
       }
     }
 
-    // Epilogue: lane (l16, q) owns row 16*rb + l16, columns co0 + 16*cb + 4q .. +3.
+    // Epilogue: lane (l16, q) owns row 16*rb + l16, columns co0 + 16*cb + 4q .. +3.  Residual
+    // values are all loaded before the first store (rows past N read row 0, not stored); each
+    // element is read and written by the same lane, so the output may alias the residual.
+    struct alignas(4 * sizeof(T)) V4 {
+      T v[4];
+    };
+    int32_t rows[4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) rows[rb] = __shfl(row_c, rb * 16 + l16, 64);
+    V4 rt[4][2];
+    if (EPI == TSC_EPI_BIAS_RESIDUAL) {
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+          rt[rb][cb] = *(const V4*)(residual + (int64_t)(rows[rb] >= 0 ? rows[rb] : 0) * co_total +
+                                    co0 + cb * 16 + 4 * q);
+    }
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
-      const int32_t row = __shfl(row_c, rb * 16 + l16, 64);
+      const int32_t row = rows[rb];
       if (row < 0) continue;
 #pragma unroll
       for (int cb = 0; cb < 2; ++cb) {
@@ -451,13 +468,9 @@ __global__ void __launch_bounds__(64 * kGWaves)
         float xv[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) xv[i] = acc[rb][cb][i] + bv[cb][i];
-        struct alignas(4 * sizeof(T)) V4 {
-          T v[4];
-        };
         if (EPI == TSC_EPI_BIAS_RESIDUAL) {
-          const V4 rt = *(const V4*)(residual + (int64_t)row * co_total + c);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) xv[i] += (float)rt.v[i];
+          for (int i = 0; i < 4; ++i) xv[i] += (float)rt[rb][cb].v[i];
         }
         V4 y;
 #pragma unroll
