@@ -13,6 +13,16 @@ __device__ __forceinline__ float rn_wave_sum(float v) {
   return v;
 }
 
+// The butterfly restricted to aligned groups of G lanes.  When only the first n <= G lanes of a
+// group hold nonzero values it returns the bits rn_wave_sum returns for those values in lanes
+// 0..n-1 of a wave: the wave's wider steps only add exact zeros.
+template <int G>
+__device__ __forceinline__ float rn_group_sum(float v) {
+#pragma unroll
+  for (int off = G / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
 __device__ __forceinline__ float rn_silu(float x) { return x * (1.0f / (1.0f + __expf(-x))); }
 
 }  // namespace tsc

@@ -9,7 +9,10 @@
 // LayerNorm runs one wave64 per row: each lane owns C/64 strided 16-byte vectors, the row is
 // read from HBM once and kept in registers (C <= 64 lanes * MAXV vectors * elements per vector),
 // mean and variance come from two wave reductions over those registers, and the normalised row
-// is written once.  Longer or unaligned rows take a three-pass strided kernel.
+// is written once.  Rows of at most 32 vectors share a wave (one lane group per row, the same
+// bits); longer or unaligned rows take a three-pass strided kernel.
+
+#include <type_traits>
 
 #include "rownorm.h"
 #include "tsc_internal.h"
@@ -115,6 +118,63 @@ __global__ void __launch_bounds__(256)
   }
 }
 
+// Rows of at most 32 16-byte vectors: 64 / LPR rows per wave, LPR lanes per row (LPR = the power
+// of two >= the row's vector count), reduced over the lane group.  Lane i of a group holds the
+// row's vector i, as lane i of a wave does in layernorm_kernel, and the group butterfly gives the
+// same bits as the wave butterfly there (the wave's wider steps add only zeros), so the result
+// is bit-identical to one row per wave without idling the lanes past the row's vectors.
+template <typename T, int LPR>
+__global__ void __launch_bounds__(256)
+    layernorm_rows_kernel(const T* x, int64_t N, int32_t C, const T* __restrict__ gamma,
+                          const T* __restrict__ beta, float eps, int32_t apply_silu, T* y) {
+  constexpr int VN = Vec<T>::n, RPW = 64 / LPR;
+  const int lane = threadIdx.x & 63, vi = lane % LPR;
+  const int64_t row0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW;
+  if (row0 >= N) return;  // uniform per wave
+  const int64_t row = row0 + lane / LPR;
+  const int nvec = C / VN;
+  const bool live = row < N && vi < nvec;
+  float v[VN];
+  if (live) {
+    unpack<T>(((const uint4*)(x + row * C))[vi], v);
+  } else {
+#pragma unroll
+    for (int e = 0; e < VN; ++e) v[e] = 0.f;
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < VN; ++e) s += v[e];
+  const float mean = rn_group_sum<LPR>(s) / (float)C;
+  float q = 0.f;
+  if (vi < nvec) {
+#pragma unroll
+    for (int e = 0; e < VN; ++e) {
+      const float d = v[e] - mean;
+      q += d * d;
+    }
+  }
+  const float var = rn_group_sum<LPR>(q) / (float)C;
+  const float inv = 1.0f / sqrtf(var + eps);
+  if (!live) return;
+  float g[VN], b[VN];
+  if (gamma) unpack<T>(((const uint4*)gamma)[vi], g);
+  else
+#pragma unroll
+    for (int e = 0; e < VN; ++e) g[e] = 1.f;
+  if (beta) unpack<T>(((const uint4*)beta)[vi], b);
+  else
+#pragma unroll
+    for (int e = 0; e < VN; ++e) b[e] = 0.f;
+  float o[VN];
+#pragma unroll
+  for (int e = 0; e < VN; ++e) {
+    const float t = (v[e] - mean) * inv * g[e] + b[e];
+    o[e] = apply_silu ? silu_f(t) : t;
+  }
+  __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, pack<T>(o)),
+                              (u32x4_t*)(y + row * C) + vi);
+}
+
 // Generic-length fallback (any C): one wave per row, three strided passes over global memory.
 template <typename T>
 __global__ void __launch_bounds__(256)
@@ -179,7 +239,18 @@ int ln_dispatch(tsc_ctx* ctx, const T* x, int64_t N, int32_t C, const T* g, cons
                       (!b || aligned16(b));
   const int nvec = C / VN;
   ProfScope p(ctx, silu ? "layernorm_silu" : "layernorm");
-  if (vec_ok && nvec <= 64 * 2)
+  auto rows = [&](auto lpr) {
+    constexpr int L = decltype(lpr)::value;
+    const unsigned g2 = (unsigned)((N + 4 * (64 / L) - 1) / (4 * (64 / L)));
+    layernorm_rows_kernel<T, L><<<g2, 256, 0, ctx->stream>>>(x, N, C, g, b, eps, silu, y);
+  };
+  if (vec_ok && nvec <= 1) rows(std::integral_constant<int, 1>());
+  else if (vec_ok && nvec <= 2) rows(std::integral_constant<int, 2>());
+  else if (vec_ok && nvec <= 4) rows(std::integral_constant<int, 4>());
+  else if (vec_ok && nvec <= 8) rows(std::integral_constant<int, 8>());
+  else if (vec_ok && nvec <= 16) rows(std::integral_constant<int, 16>());
+  else if (vec_ok && nvec <= 32) rows(std::integral_constant<int, 32>());
+  else if (vec_ok && nvec <= 64 * 2)
     layernorm_kernel<T, 2><<<grid, 256, 0, ctx->stream>>>(x, N, C, g, b, eps, silu, y);
   else if (vec_ok && nvec <= 64 * 8)
     layernorm_kernel<T, 8><<<grid, 256, 0, ctx->stream>>>(x, N, C, g, b, eps, silu, y);
