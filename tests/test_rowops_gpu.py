@@ -53,6 +53,30 @@ def test_layernorm_silu_shapes(pkg, dev, dtype, n, c, affine):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_layernorm_row_groups(pkg, dev, dtype):
+    """Rows of 1..33 16-byte vectors around every lane-group size of the grouped pass (several
+    rows per wave for <= 32 vectors, one row per wave above), a row count that leaves the last
+    wave partly empty, affine and plain, against the fp64 layer norm; in-place as well."""
+    per = 4 if dtype == torch.float32 else 8  # elements per 16-byte vector
+    rng = np.random.default_rng(5)
+    for nvec in (1, 2, 3, 5, 8, 16, 17, 32, 33):
+        c = nvec * per
+        n = 3 * (64 // min(64, 1 << (nvec - 1).bit_length())) * 4 + 5
+        x, x64 = _r(rng.standard_normal((n, c)) * 1.5 - 0.2, dtype, dev)
+        g, g64 = _r(rng.uniform(0.5, 1.5, c), dtype, dev)
+        b, b64 = _r(rng.standard_normal(c) * 0.1, dtype, dev)
+        for affine in (False, True):
+            gg, bb = (g, b) if affine else (None, None)
+            gr, br = (g64, b64) if affine else (None, None)
+            y = pkg.layer_norm(x, gg, bb, 1e-6, silu=True).float().cpu().numpy()
+            err = rel_err(y, oracle.layernorm(x64, gr, br, 1e-6, silu=True))
+            assert err <= TOL[dtype] * 4, (nvec, affine, err)
+        x2 = x.clone()
+        pkg.layer_norm(x2, None, None, 1e-6, out=x2)
+        assert rel_err(x2.float().cpu().numpy(), oracle.layernorm(x64, None, None, 1e-6)) <= TOL[dtype] * 4
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 def test_silu_add(pkg, dev, dtype):
     rng = np.random.default_rng(1)
     x, x64 = _r(rng.standard_normal(100003) * 4, dtype, dev)
