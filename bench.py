@@ -92,7 +92,7 @@ def kernel_times(ctx, fn, steps: int) -> dict:
 ROCPROF_NAME = {"map_fill": "fill_columns_kernel<bitmap>", "map_mark": "mark_kernel<int32>",
                 "map_place": "place_kernel<int32>", "radix_fill": "fill_window_kernel<int32>",
                 "radix_buckets": "bucket_sort_kernel<int32>",
-                "radix_partition": "partition_kernel<int32>", "radix_pack": "pack_kernel<int32>",
+                "radix_partition": "partition_kernel<int32>", "radix_pack": "pack_sort_kernel<int32>",
                 "radix_scan": "scan_kernel"}
 
 

@@ -2,23 +2,22 @@
 //
 // Same outputs as the bitmap path (sorted unique keys, their rows, the (N,27) neighbor table; see
 // map_build.hip for the semantics and reference citations).  Keys have nbits = bitlen(cells-1)
-// bits; the top TB = min(nbits, 10) bits select one of 2^TB buckets.  Steps:
-//   pack       coords -> (key, row) in input order, per-8192-row tile histogram of the bucket digit
-//              and a per-tile out-of-range flag.  Out-of-range coordinates are clamped to the
-//              last cell (so every key stays below 2^nbits) and reported through the flag.
-//   scan       exclusive scan over tiles of each bucket's counts (one block per bucket), bucket
-//              totals; block 0 folds the tile flags into the status word.
-//   partition  stable scatter of (key, row) by bucket: wave-ballot multisplit ranks inside a
-//              tile (one ballot per digit bit -> peer mask -> popcount), the tile is reordered
-//              by digit in LDS and written as contiguous runs.
-//   bucket     one block per bucket: stable LSD passes over the bucket's remaining bits (at most
-//              9 per pass) between two L2-resident copies of the bucket, the last pass writing
-//              the outputs; then col_start[c] for the (b,x,y) columns whose first key c*Z falls
-//              in the bucket's key range, by binary search of the sorted bucket in LDS.
+// bits; the top TB = min(nbits, 10) bits select one of 2^TB buckets.  Steps of the map build (up
+// to 2048 tiles of 8192 voxels, i.e. 16.7 M voxels):
+//   pack_sort  coords -> (key, row), reordered inside each 8192-row tile by bucket digit and
+//              written back over the tile, with the tile's digit starts and an out-of-range flag
+//              (out-of-range coordinates are clamped to the last cell, so every key stays below
+//              2^nbits, and reported through the flag).
+//   bucket     one block per bucket: gathers the bucket's run from every tile, sorts it by an
+//              LDS bitmap of its key range (rank = set bits below; stable LSD passes for repeated
+//              keys or buckets past 65536) and writes the sorted keys and rows, plus col_start[c]
+//              for the (b,x,y) columns whose first key c*Z falls in the bucket's key range; block
+//              0 folds the tile flags into the status word.
 //   fill       window fill from LDS (below), or the column-parallel fill over the whole sorted
 //              array when the column table would be much larger than the voxel set.
-// The gather plan sorts its rows by Morton key with the same pack / scan / partition / bucket
-// stages (sort_rows_morton, no column starts).
+// Larger sets, and the gather plan's Morton sort (sort_rows_morton, no column starts; its buckets
+// are uneven), run pack (histograms only), scan (per-bucket offsets over tiles), partition
+// (scatter into contiguous buckets) and the same bucket kernel reading the partitioned copy.
 
 #include <algorithm>
 #include <type_traits>
@@ -302,6 +301,93 @@ __global__ void __launch_bounds__(PT)
   }
 }
 
+// Gather pipeline (at most kGatherTiles tiles): pack and a tile-local sort by bucket digit in one
+// kernel.  The tile's (key, row) pairs are formed as in pack_kernel, reordered by digit in LDS
+// (slots from LDS atomics, as in partition_kernel) and written back over the tile's own range as
+// one coalesced run.  toff[tile * (nb + 1) + d] = the tile's first position of digit d (d <= nb,
+// toff[nb] = the tile's size), so bucket d's elements are the runs [toff[d], toff[d + 1]) of
+// every tile, and its start in the sorted output is the sum of the tiles' toff[d].  No global
+// scatter and no scan launch: the bucket kernel gathers the runs itself.
+constexpr int kGatherTiles = 2048;  // runs per bucket: 8 per thread of the bucket kernel
+
+template <typename K, typename Gen>
+__global__ void __launch_bounds__(PT)
+    pack_sort_kernel(const int4* __restrict__ coords, int64_t N, Gen gen, int shift, int dbits,
+                     K* __restrict__ ktile, int32_t* __restrict__ vtile, int* __restrict__ toff,
+                     int ntiles, int* __restrict__ oob_tile) {
+  constexpr int PDPT = NBMAX / PT;
+  __shared__ int lcnt[NBMAX];
+  __shared__ int dstart[NBMAX];
+  __shared__ int wsum[PT / 64];
+  __shared__ K sk[PTILE];
+  __shared__ int32_t sv[PTILE];
+  const int nb = 1 << dbits, mask = nb - 1;
+  const int tid = threadIdx.x;
+  for (int i = tid; i < NBMAX; i += PT) lcnt[i] = 0;
+  __syncthreads();
+  const int64_t tile0 = (int64_t)blockIdx.x * PTILE;
+  const int64_t rem = N - tile0;
+  const int tile_n = rem < PTILE ? (int)rem : PTILE;
+  // Every coordinate load is issued before the first use (indices past the tile re-read its
+  // last element, never used).
+  int4 c[PI];
+#pragma unroll
+  for (int j = 0; j < PI; ++j) c[j] = coords[tile0 + min(j * PT + tid, tile_n - 1)];
+  K kk[PI];
+  int slot[PI];
+  int oob = 0;
+#pragma unroll
+  for (int j = 0; j < PI; ++j) {
+    K key = (K)0;
+    slot[j] = 0;
+    if (j * PT + tid < tile_n) {
+      if (!gen(c[j], &key)) oob = 1;
+      slot[j] = atomicAdd(&lcnt[digit_of<K>(key, shift, mask)], 1);  // LDS atomic
+    }
+    kk[j] = key;
+  }
+  oob = __syncthreads_or(oob);
+  // Tile-local digit starts: thread t owns digits [t*PDPT, (t+1)*PDPT).
+  int loc[PDPT];
+  int tsum = 0;
+#pragma unroll
+  for (int q = 0; q < PDPT; ++q) {
+    const int d = tid * PDPT + q;
+    loc[q] = d < nb ? lcnt[d] : 0;
+    tsum += loc[q];
+  }
+  int dummy;
+  int pre = block_excl_scan<PT / 64>(tsum, wsum, &dummy);
+#pragma unroll
+  for (int q = 0; q < PDPT; ++q) {
+    const int d = tid * PDPT + q;
+    if (d < nb) {
+      dstart[d] = pre;
+      toff[(int64_t)blockIdx.x * (nb + 1) + d] = pre;
+    }
+    pre += loc[q];
+  }
+  if (tid == 0) {
+    toff[(int64_t)blockIdx.x * (nb + 1) + nb] = tile_n;
+    oob_tile[blockIdx.x] = oob;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < PI; ++j) {
+    const int i = j * PT + tid;
+    if (i < tile_n) {
+      const int p = dstart[digit_of<K>(kk[j], shift, mask)] + slot[j];
+      sk[p] = kk[j];
+      sv[p] = (int32_t)(tile0 + i);
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < tile_n; i += PT) {
+    ktile[tile0 + i] = sk[i];
+    vtile[tile0 + i] = sv[i];
+  }
+}
+
 // First index in [lo, hi) with keys[idx] >= t.
 template <typename K>
 __device__ __forceinline__ int64_t lower_bound(const K* keys, int64_t lo, int64_t hi, K t) {
@@ -366,14 +452,27 @@ __device__ __forceinline__ void wave_offsets(int (*wcnt)[LNB], int (&cnt)[LPT]) 
 constexpr int kBitmapBits = 17;
 constexpr int kBitmapWords = (1 << kBitmapBits) / 32;
 
+// Source of the buckets in the gather pipeline: pack_sort_kernel's tile-sorted pairs and digit
+// starts (ktile == nullptr: the partitioned layout, bucket b at [bstart[b], + totals[b]) of k0).
+template <typename K>
+struct GatherSrc {
+  const K* ktile;
+  const int32_t* vtile;
+  const int* toff;
+  int ntiles;
+  const int* oob_tile;  // folded into *status by block 0
+  uint32_t* status;
+};
+
 template <typename K>
 __global__ void __launch_bounds__(RT)
     bucket_sort_kernel(K* k0, int32_t* v0, K* k1, int32_t* v1, K* __restrict__ kout,
                        int32_t* __restrict__ vout, const int* __restrict__ totals,
                        const int* __restrict__ bstart, int nbk,
                        int lb, int64_t cells, int64_t Z, int64_t ncol, int64_t n,
-                       int32_t* __restrict__ col_start) {
-  // smem: the key bitmap, or the LSD digit counters run[LNB] + wcnt[WAVES][LNB].
+                       int32_t* __restrict__ col_start, GatherSrc<K> gs) {
+  // smem: the key bitmap, or the LSD digit counters run[LNB] + wcnt[WAVES][LNB]; before either,
+  // the gather pipeline's run table of the bucket.
   __shared__ __attribute__((aligned(16))) uint32_t smem[kBitmapWords];
   __shared__ __attribute__((aligned(16))) uint16_t wpre[kBitmapWords];  // set bits before each word
   __shared__ int wsum[WAVES];
@@ -383,34 +482,111 @@ __global__ void __launch_bounds__(RT)
   int(*wcnt)[LNB] = (int(*)[LNB])((int*)smem + LNB);
   const int tid = threadIdx.x;
   const int b = blockIdx.x;
-  const int64_t start = bstart[b];
-  const int size = totals[b];
   const int passes = (lb + LBITS - 1) / LBITS;
   const int pbits = passes ? (lb + passes - 1) / passes : 0;
   const K lmask = (K)(((uint64_t)1 << lb) - 1);
+  const bool gather = gs.ktile != nullptr;
+  int64_t start;
+  int size;
+  // Gather pipeline: run t of the bucket (tile t's elements of digit b, thread t % RT's run
+  // k = t / RT) holds the bucket's elements [rb0[k], rb0[k] + rl[k]), read from tile t at
+  // t*PTILE + ra[k].  The source positions of RTILE elements at a time are expanded into LDS
+  // (pos[i]), so each element costs one LDS read.
+  constexpr int kRunsPerThread = (kGatherTiles + RT - 1) / RT;
+  int* const pos = (int*)smem;  // [RTILE] expanded source positions, before the bitmap
+  static_assert(RTILE <= kBitmapWords, "expanded positions fit the bitmap's words");
+  int ra[kRunsPerThread], rl[kRunsPerThread], rb0[kRunsPerThread];
+  if (gather) {
+    const int nt = gs.ntiles;
+    int carry = 0, below = 0;
+#pragma unroll
+    for (int k = 0; k < kRunsPerThread; ++k) {
+      ra[k] = rl[k] = rb0[k] = 0;
+      if (k * RT >= nt) continue;  // uniform
+      const int t = k * RT + tid;
+      if (t < nt) {
+        ra[k] = gs.toff[(int64_t)t * (nbk + 1) + b];
+        rl[k] = gs.toff[(int64_t)t * (nbk + 1) + b + 1] - ra[k];
+      }
+      int tot;
+      rb0[k] = carry + block_excl_scan(rl[k], wsum, &tot);
+      carry += tot;
+      below += ra[k];
+    }
+    int tot_below;
+    (void)block_excl_scan(below, wsum, &tot_below);  // elements of smaller digits: the start
+    start = tot_below;
+    size = carry;
+    if (b == 0 && gs.status) {
+      int any = 0;
+      for (int t = tid; t < nt; t += RT) any |= gs.oob_tile[t];
+      any = __syncthreads_or(any);
+      if (tid == 0) gs.status[0] = any ? (uint32_t)TSC_MAP_OUT_OF_RANGE : 0u;
+    }
+  } else {
+    start = bstart[b];
+    size = totals[b];
+  }
+  // 16-bit word prefixes hold ranks below 65536: larger buckets take the LSD path.
+  const bool bitmap_ok = size <= 65536 && lb <= kBitmapBits && passes > 0;
+  // A bucket of at most RTILE elements stays in registers; a larger one is read in chunks of
+  // RTILE twice (bits, then ranks) and written by rank straight to the outputs.
+  const bool in_regs = bitmap_ok && size <= RTILE;
+  K kk[RI];
+  int32_t vv[RI];
+  if (gather) {
+    const int nt = gs.ntiles;
+    // Chunks of RTILE elements (one chunk when the bucket stays in registers): positions of the
+    // chunk's elements into LDS, then one read per element.
+    for (int c0 = 0; c0 < size; c0 += RTILE) {  // uniform
+      const int c1 = min(size, c0 + RTILE);
+#pragma unroll
+      for (int k = 0; k < kRunsPerThread; ++k) {
+        const int t = k * RT + tid;
+        if (t >= nt) continue;
+        const int lo = max(rb0[k], c0), hi = min(rb0[k] + rl[k], c1);
+        for (int e = lo; e < hi; ++e) pos[e - c0] = t * PTILE + ra[k] + (e - rb0[k]);
+      }
+      __syncthreads();
+      if (in_regs) {
+#pragma unroll
+        for (int j = 0; j < RI; ++j) {
+          const int i = j * RT + tid;
+          if (i < size) {
+            const int q = pos[i];
+            kk[j] = gs.ktile[q];
+            vv[j] = gs.vtile[q];
+          }
+        }
+      } else {
+        // Every other path reads the bucket from (k0, v0): assemble it there first.
+        for (int i = c0 + tid; i < c1; i += RT) {
+          const int q = pos[i - c0];
+          k0[start + i] = gs.ktile[q];
+          v0[start + i] = gs.vtile[q];
+        }
+      }
+      __syncthreads();
+    }
+  } else if (in_regs) {
+#pragma unroll
+    for (int j = 0; j < RI; ++j) {
+      const int i = j * RT + tid;
+      if (i < size) {
+        kk[j] = k0[start + i];
+        vv[j] = v0[start + i];
+      }
+    }
+  }
 
   bool by_bitmap = false;
-  // 16-bit word prefixes hold ranks below 65536: larger buckets take the LSD path.
-  if (size <= 65536 && lb <= kBitmapBits && passes > 0) {
+  if (bitmap_ok) {
     const int nwords = ((1 << lb) + 31) / 32;
     for (int i = tid; i < nwords; i += RT) bits[i] = 0u;
     __syncthreads();
-    // A bucket of at most RTILE elements stays in registers; a larger one is read in chunks of
-    // RTILE twice (bits, then ranks) and written by rank straight to the outputs.
-    const bool in_regs = size <= RTILE;
-    K kk[RI];
-    int32_t vv[RI];
     int loc[RI];
     int dup = 0;
     if (in_regs) {
-#pragma unroll
-      for (int j = 0; j < RI; ++j) {
-        const int i = j * RT + tid;
-        if (i < size) {
-          kk[j] = k0[start + i];
-          vv[j] = v0[start + i];
-        }
-      }
 #pragma unroll
       for (int j = 0; j < RI; ++j) {
         const int i = j * RT + tid;
@@ -556,6 +732,16 @@ __global__ void __launch_bounds__(RT)
         }
       }
       by_bitmap = true;
+    } else if (gather && in_regs) {
+      // A repeated key: the LSD path reads the bucket from (k0, v0).
+#pragma unroll
+      for (int j = 0; j < RI; ++j) {
+        const int i = j * RT + tid;
+        if (i < size) {
+          k0[start + i] = kk[j];
+          v0[start + i] = vv[j];
+        }
+      }
     }
   }
   if (!by_bitmap) {
@@ -997,32 +1183,51 @@ constexpr int kFillRounds = 1024 / kFillThreads;  // 112 voxels per block
 // per-(bucket, tile) counts, bucket totals and starts, per-tile out-of-range flags.
 template <typename K>
 struct SortBufs {
-  K *kA, *kB;
-  int32_t *vA, *vB;
+  K *kA, *kB, *kC;
+  int32_t *vA, *vB, *vC;
   int *counts, *totals, *oob_tile, *bstart;
-  static size_t bytes(int64_t N, int nb) {
+  // The gather pipeline keeps the tile-sorted pairs (kA, vA) intact while buckets are sorted, so
+  // its LSD passes ping-pong between (kB, vB) and a third copy (kC, vC); counts holds the tiles'
+  // digit starts, ntiles x (nb + 1).
+  // want_gather: the caller's keys suit the gather pipeline (see sort_stages).
+  static bool gather(int64_t N, bool want_gather) {
+    return want_gather && (N + PTILE - 1) / PTILE <= kGatherTiles;
+  }
+  static size_t bytes(int64_t N, int nb, bool want_gather) {
     const int64_t ntiles = (N + PTILE - 1) / PTILE;
-    return 2 * align_up((size_t)N * sizeof(K), 256) + 2 * align_up((size_t)N * 4, 256) +
-           align_up((size_t)nb * ntiles * 4, 256) + 2 * align_up((size_t)nb * 4, 256) +
+    const int copies = gather(N, want_gather) ? 3 : 2;
+    return copies * (align_up((size_t)N * sizeof(K), 256) + align_up((size_t)N * 4, 256)) +
+           align_up((size_t)(nb + 1) * ntiles * 4, 256) + 2 * align_up((size_t)nb * 4, 256) +
            align_up((size_t)ntiles * 4, 256);
   }
-  void carve(Carve& cv, int64_t N, int nb) {
+  void carve(Carve& cv, int64_t N, int nb, bool want_gather) {
     const int64_t ntiles = (N + PTILE - 1) / PTILE;
     kA = cv.take<K>(N);
     vA = cv.take<int32_t>(N);
     kB = cv.take<K>(N);
     vB = cv.take<int32_t>(N);
-    counts = cv.take<int>((int64_t)nb * ntiles);
+    kC = nullptr;
+    vC = nullptr;
+    if (gather(N, want_gather)) {
+      kC = cv.take<K>(N);
+      vC = cv.take<int32_t>(N);
+    }
+    counts = cv.take<int>((int64_t)(nb + 1) * ntiles);
     totals = cv.take<int>(nb);
     oob_tile = cv.take<int>(ntiles);
     bstart = cv.take<int>(nb);
   }
 };
 
-// Sort of (gen(coords[i]), i) for i < N (N > 0) by keys below 2^nbits, at most TBMAX bucket bits:
-// pack, scan, partition, buckets.  Sorted pairs go to (kOut, vOut), the column starts to cols
-// when it is not null (for the map's (b, x, y) columns of Z keys each), the out-of-range flag to
-// *status.  `tag` prefixes the profiler names.
+// Sort of (gen(coords[i]), i) for i < N (N > 0) by keys below 2^nbits, at most TBMAX bucket bits.
+// Buffers carved for the gather pipeline (up to kGatherTiles tiles): pack with the tile-local
+// digit sort, then buckets gathering their runs -- two launches, for evenly filled buckets such
+// as the map's x-slab buckets of a surface (1.5 M-voxel shell: 39 against 54 us for the four
+// launches below).  Otherwise pack, scan, partition, buckets: the Morton order's buckets hold up
+// to 12 k voxels, which the gather path assembles one block per bucket (63 against 49 us for
+// partition + buckets).  Sorted pairs go to (kOut, vOut), the column starts to cols when it is
+// not null (for the map's (b, x, y) columns of Z keys each), the out-of-range flag to *status.
+// names[] are the profiler names of the four stages.
 template <typename K, typename Gen>
 void sort_stages(tsc_ctx* ctx, const int32_t* coords, int64_t N, Gen gen, int nbits,
                  const SortBufs<K>& sb, K* kOut, int32_t* vOut, int64_t cells, int64_t Z,
@@ -1032,6 +1237,18 @@ void sort_stages(tsc_ctx* ctx, const int32_t* coords, int64_t N, Gen gen, int nb
   const int nbk = 1 << tb;
   const int64_t ntiles = (N + PTILE - 1) / PTILE;
   hipStream_t s = ctx->stream;
+  if (sb.kC) {  // carved for the gather pipeline
+    {
+      ProfScope p(ctx, names[0]);
+      pack_sort_kernel<K, Gen><<<(unsigned)ntiles, PT, 0, s>>>(
+          (const int4*)coords, N, gen, lb, tb, sb.kA, sb.vA, sb.counts, (int)ntiles, sb.oob_tile);
+    }
+    ProfScope ps(ctx, names[3]);
+    bucket_sort_kernel<K><<<(unsigned)nbk, RT, 0, s>>>(
+        sb.kB, sb.vB, sb.kC, sb.vC, kOut, vOut, nullptr, nullptr, nbk, lb, cells, Z, ncol, N,
+        cols, GatherSrc<K>{sb.kA, sb.vA, sb.counts, (int)ntiles, sb.oob_tile, status});
+    return;
+  }
   {
     ProfScope p(ctx, names[0]);
     pack_kernel<K, Gen><<<(unsigned)ntiles, PT, 0, s>>>(
@@ -1049,9 +1266,9 @@ void sort_stages(tsc_ctx* ctx, const int32_t* coords, int64_t N, Gen gen, int nb
   }
   {
     ProfScope ps(ctx, names[3]);
-    bucket_sort_kernel<K><<<(unsigned)nbk, RT, 0, s>>>(sb.kB, sb.vB, sb.kA, sb.vA, kOut, vOut,
-                                                        sb.totals, sb.bstart, nbk, lb, cells, Z,
-                                                        ncol, N, cols);
+    bucket_sort_kernel<K><<<(unsigned)nbk, RT, 0, s>>>(
+        sb.kB, sb.vB, sb.kA, sb.vA, kOut, vOut, sb.totals, sb.bstart, nbk, lb, cells, Z, ncol, N,
+        cols, GatherSrc<K>{nullptr, nullptr, nullptr, 0, nullptr, nullptr});
   }
 }
 
@@ -1063,7 +1280,7 @@ int radix_impl(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t B, int32_
   const int nbits = std::max(1, bit_length((uint64_t)(cells - 1)));
   const int64_t ncol = (int64_t)B * X * Y;
   const bool use_cols = ncol <= std::max<int64_t>(16 * N, int64_t(1) << 22);
-  size_t need = SortBufs<K>::bytes(N, NBMAX) +
+  size_t need = SortBufs<K>::bytes(N, NBMAX, true) +
                 (use_cols ? align_up((size_t)(ncol + 1) * 4, 256) : 0);
   if (!keys_out) need += align_up((size_t)N * sizeof(K), 256);
   if (!perm_out) need += align_up((size_t)N * 4, 256);
@@ -1072,7 +1289,7 @@ int radix_impl(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t B, int32_
   if (st) return st;
   Carve cv(ws);
   SortBufs<K> sb;
-  sb.carve(cv, N, NBMAX);
+  sb.carve(cv, N, NBMAX, true);
   int32_t* cols = use_cols ? cv.take<int32_t>(ncol + 1) : nullptr;
   K* kOut = keys_out ? (K*)keys_out : cv.take<K>(N);
   int32_t* vOut = perm_out ? perm_out : cv.take<int32_t>(N);
@@ -1129,14 +1346,14 @@ namespace {
 template <typename K>
 int morton_impl(tsc_ctx* ctx, const int32_t* coords, int64_t N, int bits, int shift, int nbits,
                 int32_t* rows_out) {
-  const size_t need = SortBufs<K>::bytes(N, NBMAX) + align_up((size_t)N * sizeof(K), 256) +
+  const size_t need = SortBufs<K>::bytes(N, NBMAX, false) + align_up((size_t)N * sizeof(K), 256) +
                       256;
   void* ws;
   int st = workspace(ctx, need, &ws);
   if (st) return st;
   Carve cv(ws);
   SortBufs<K> sb;
-  sb.carve(cv, N, NBMAX);
+  sb.carve(cv, N, NBMAX, false);
   K* kOut = cv.take<K>(N);
   uint32_t* status = cv.take<uint32_t>(1);  // the scan's flag word; Morton keys never set it
   const uint64_t mask = nbits >= 64 ? ~0ull : ((1ull << nbits) - 1);
