@@ -120,6 +120,34 @@ def test_map_bucket_over_65536(pkg, dev, method):
     _check(m, c, 1, (512, 512, 512), (1, 1, 1))
 
 
+@pytest.mark.parametrize("xs", [256, 257])
+def test_map_dense_box_at_the_sort_limit(pkg, dev, xs):
+    """Dense xs x 256 x 256 boxes, shuffled: 2048 sorting tiles of 8192 voxels (xs = 256, the most
+    the gathering sort takes: every bucket thread holds eight runs) and 2056 tiles (xs = 257, the
+    four-launch sort).  16.8 M voxels are too many for the oracle; a dense box fixes the answer:
+    the sorted keys are 0..N-1, perm inverts the shuffle, and neighbor v of a row is the row of the
+    in-box cell at offset v, else -1."""
+    X, Y, Z = 260, 256, 256
+    n = xs * Y * Z
+    print(f"  dense box {xs}x{Y}x{Z} N={n}", flush=True)
+    key_of_row = torch.randperm(n, generator=torch.Generator().manual_seed(11)).to(dev)
+    x, y, z = key_of_row // (Y * Z), (key_of_row // Z) % Y, key_of_row % Z
+    coords = torch.stack([torch.zeros_like(x), x, y, z], 1).int()
+    m = pkg.build_neighbor_map(coords, (X, Y, Z), 1, method="radix")
+    torch.cuda.synchronize()
+    assert torch.equal(m.keys.long(), torch.arange(n, device=dev))
+    row_of_key = torch.empty_like(key_of_row)
+    row_of_key[key_of_row] = torch.arange(n, device=dev)
+    assert torch.equal(m.perm.long(), row_of_key)
+    for v in range(27):
+        nx, ny, nz = x + (v // 9 - 1), y + ((v // 3) % 3 - 1), z + (v % 3 - 1)
+        inside = (nx >= 0) & (nx < xs) & (ny >= 0) & (ny < Y) & (nz >= 0) & (nz < Z)
+        nkey = ((nx * Y + ny) * Z + nz).clamp(0, n - 1)
+        want = torch.where(inside, row_of_key[nkey], torch.full_like(nkey, -1))
+        assert torch.equal(m.nbr[:, v].long(), want), f"tap {v}"
+    del m
+
+
 def test_map_empty(pkg, dev):
     c = torch.zeros((0, 4), dtype=torch.int32, device=dev)
     m = pkg.build_neighbor_map(c, (4, 4, 4), 1)
