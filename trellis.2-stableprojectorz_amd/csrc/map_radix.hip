@@ -1179,8 +1179,9 @@ inline int bit_length(uint64_t v) {
 constexpr int kFillThreads = 256;
 constexpr int kFillRounds = 1024 / kFillThreads;  // 112 voxels per block
 
-// Sort buffers carved from one workspace: (kA, vA) and (kB, vB) ping-pong copies of the pairs,
-// per-(bucket, tile) counts, bucket totals and starts, per-tile out-of-range flags.
+// Sort buffers carved from one workspace: (kA, vA) and (kB, vB) ping-pong copies of the pairs
+// (plus (kC, vC) for the gather pipeline), per-(bucket, tile) counts or the tiles' digit starts,
+// bucket totals and starts, per-tile out-of-range flags.
 template <typename K>
 struct SortBufs {
   K *kA, *kB, *kC;
