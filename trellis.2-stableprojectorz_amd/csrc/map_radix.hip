@@ -481,7 +481,11 @@ __global__ void __launch_bounds__(RT)
   int* run = (int*)smem;
   int(*wcnt)[LNB] = (int(*)[LNB])((int*)smem + LNB);
   const int tid = threadIdx.x;
-  const int b = blockIdx.x;
+  // Block i runs on XCD i mod 8: each XCD takes a contiguous eighth of the buckets, so the
+  // neighboring buckets that share cache lines of the tiles' runs (and of the digit starts) are
+  // fetched into one L2.
+  const int b = (nbk & 7) == 0 ? (int)(blockIdx.x & 7) * (nbk >> 3) + (int)(blockIdx.x >> 3)
+                               : (int)blockIdx.x;
   const int passes = (lb + LBITS - 1) / LBITS;
   const int pbits = passes ? (lb + passes - 1) / passes : 0;
   const K lmask = (K)(((uint64_t)1 << lb) - 1);
