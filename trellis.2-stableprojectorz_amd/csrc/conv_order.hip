@@ -10,7 +10,7 @@
 // their leading taps sit next to each other, and consecutive ones differ in as few taps as the
 // sequence allows, so a tile's union of taps stays close to one row's.  Ties keep key order.
 //
-// Stable LSD radix sort, three passes of <= 9 bits, over tiles of 16384 rows (16 per window):
+// Stable LSD radix sort, three passes of <= 9 bits, over tiles of 4096 rows (64 per window):
 //   rowmask  per row, reading the map in row order: the Gray rank of its mask
 //   mask     key = rowmask[perm[i]], val = perm[i]; tile histogram of digit 0
 //   scan     per window: digit-major, tile-minor exclusive offsets of the 16 tiles' counts
@@ -33,9 +33,12 @@ namespace tsc {
 namespace {
 
 constexpr int kOrdThreads = 1024;
-constexpr int kOrdItems = 16;
-constexpr int kOrdTile = kOrdThreads * kOrdItems;  // 16384 rows per tile
-constexpr int kOrdTilesPerWin = 16;                // 262144 rows per window
+// 4096-row tiles: 370 blocks per pass at 1.5 M rows and 60 at 243 k, against 93 / 15 with
+// 16384-row tiles, which left most CUs idle (conv order 254 -> 209 us at 1.5 M rows, 187 ->
+// 127 us at 243 k; 2048- and 8192-row tiles measured slower).
+constexpr int kOrdItems = 4;
+constexpr int kOrdTile = kOrdThreads * kOrdItems;  // 4096 rows per tile
+constexpr int kOrdTilesPerWin = 64;                // 262144 rows per window
 constexpr int kOrdWaves = kOrdThreads / 64;
 constexpr int kOrdDigitBits = 9;
 constexpr int kOrdBins = 1 << kOrdDigitBits;
