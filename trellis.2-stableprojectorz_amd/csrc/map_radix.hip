@@ -36,8 +36,9 @@ constexpr int NBMAX = 1 << TBMAX;   // buckets
 constexpr int LBITS = 9;            // local pass digit bits
 constexpr int LNB = 1 << LBITS;
 constexpr int LPT = LNB / RT;       // local digits owned per thread
-constexpr int PT = 512;             // pack / partition threads per block
-constexpr int PI = 16;              // pack / partition items per thread
+constexpr int PT = 1024;            // pack / partition threads per block
+constexpr int PI = 8;               // pack / partition items per thread (512 x 16: Morton pack
+                                    // 19.6 -> 14.7 us at 1.5 M voxels, the others equal)
 constexpr int PTILE = PT * PI;      // pack / partition tile
 
 template <typename K>
