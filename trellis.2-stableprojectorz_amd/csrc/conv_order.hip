@@ -123,7 +123,10 @@ __global__ void __launch_bounds__(kOrdThreads)
   if (t0 + kOrdTile <= n) {
     int32_t r[kOrdItems];
 #pragma unroll
-    for (int j = 0; j < kOrdItems; ++j) r[j] = perm ? perm[t0 + j * kOrdThreads + tid] : (int32_t)(t0 + j * kOrdThreads + tid);
+    for (int j = 0; j < kOrdItems; ++j) {
+      const int64_t i = t0 + j * kOrdThreads + tid;
+      r[j] = perm ? perm[i] : (int32_t)i;
+    }
     uint32_t m[kOrdItems];
 #pragma unroll
     for (int j = 0; j < kOrdItems; ++j) m[j] = rowmask[r[j]];
