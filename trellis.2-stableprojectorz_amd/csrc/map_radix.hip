@@ -473,7 +473,7 @@ __global__ void __launch_bounds__(RT)
                        int lb, int64_t cells, int64_t Z, int64_t ncol, int64_t n,
                        int32_t* __restrict__ col_start, GatherSrc<K> gs) {
   // smem: the key bitmap, or the LSD digit counters run[LNB] + wcnt[WAVES][LNB]; before either,
-  // the gather pipeline's run table of the bucket.
+  // the gather pipeline's expanded source positions of the bucket's elements.
   __shared__ __attribute__((aligned(16))) uint32_t smem[kBitmapWords];
   __shared__ __attribute__((aligned(16))) uint16_t wpre[kBitmapWords];  // set bits before each word
   __shared__ int wsum[WAVES];
