@@ -109,6 +109,15 @@ int tsc_map_build(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t B, int
                   int32_t Z, const int32_t kernel[3], const int32_t dilation[3], int32_t method,
                   void* keys_out, int32_t* perm_out, int32_t* nbr_out, uint32_t* status_dev);
 
+/* A measurement call, not part of the conv path: writes the (N,27) int32 table `out` with the
+ * radix map build's fill store pattern and nothing else (blocks of 112 consecutive sorted
+ * positions, 9 lanes x 12 bytes of each 108-byte row at row rows[i]; rows NULL = i; rows outside
+ * [0, N) skipped; the words are (-1, row, -1) per lane).  rows[i] is its only load.  Given the
+ * perm_out of tsc_map_build it takes as long as the fill would if finding the neighbors cost
+ * nothing: the floor of a neighbor table in the caller's row order.  Stream-ordered.
+ * No counterpart in the reference. */
+int tsc_map_write_floor(tsc_ctx* ctx, const int32_t* rows, int64_t N, int32_t* out);
+
 /* Row order for tsc_conv / tsc_conv_fused / tsc_resblock: the map's sorted rows (perm, from
  * tsc_map_build; NULL = 0..N-1), sorted inside windows of 262144 consecutive entries by the
  * reflected-binary rank of their 26-bit mask of present neighbors (ties keep the given order),
@@ -143,6 +152,10 @@ int tsc_map_gather_plan(tsc_ctx* ctx, const int32_t* coords, const int32_t* nbr,
  *   order: optional device int32 (N) permutation; rows are processed in that order (pass
  *   tsc_map_conv_order's output, or the map's perm_out for spatial locality).  NULL = 0..N-1.
  *   Results do not depend on it.
+ *   Wide tiles of 256 rows run in a longest-first order (a schedule computed from nbr and order)
+ *   that the context keeps for the next conv with the same nbr, order and N (at most 4
+ *   schedules; tsc_map_build, tsc_map_conv_order and tsc_free of either buffer drop them).  A
+ *   schedule only decides which block computes which tile, so it never changes a result.
  *   Any Ci >= 1 (Ci * element size <= 65536 bytes) and 1 <= Co <= 65536, as the reference's
  *   bounds-checked shader (conv3d_wgsl.ts:174-196).  The tuned kernels run when Ci * element size
  *   is a multiple of 32 bytes, Co a multiple of 32 and every buffer 16-byte aligned; other
@@ -170,8 +183,10 @@ int tsc_conv_fused(tsc_ctx* ctx, int32_t dtype, const void* feats, const void* w
  * of the context's growable workspace.  N must not exceed 16777216 rows (65536 tiles of 256;
  * TSC_ERR_INVALID beyond).  Every call on one GPU shares that array: calls that overlap on one
  * device (different streams or contexts) race on it; calls on one stream are ordered.
+ * The array's device address is looked up (hipGetSymbolAddress) by the first call on a context.
+ * The schedule is built on every call (the cache of tsc_conv_fused would allocate).
  * Per-kernel profiling (tsc_profile_enable) is suspended during the call.
- * No counterpart in the reference (which allocates freely, conv3d.ts:144-221). */
+ * No counterpart in the reference. */
 int tsc_conv_fused_noalloc(tsc_ctx* ctx, int32_t dtype, const void* feats, const void* weight,
                            const void* bias, const int32_t* nbr, const int32_t* order, int64_t N,
                            int32_t Ci, int32_t Co, int32_t epilogue, const void* residual,
@@ -197,7 +212,8 @@ int tsc_silu(tsc_ctx* ctx, int32_t dtype, const void* x, int64_t numel, void* y)
 int tsc_add(tsc_ctx* ctx, int32_t dtype, const void* a, const void* b, int64_t numel, void* y);
 
 /* Sparse ResBlock: out = x + conv2(silu(LN(conv1(x)+b1))) + b2, with C=Ci=Co.
- * LN uses eps and gamma/beta (NULL = 1/0).  out must not alias x.  The intermediate (N,C)
+ * LN uses eps and gamma/beta (NULL = 1/0).  out must not overlap x (TSC_ERR_INVALID if any
+ * byte of the two (N,C) ranges is shared).  The intermediate (N,C)
  * activation lives in the context's workspace. */
 int tsc_resblock(tsc_ctx* ctx, int32_t dtype, const void* x, const int32_t* nbr,
                  const int32_t* order, int64_t N, int32_t C, const void* w1, const void* b1,
@@ -206,7 +222,8 @@ int tsc_resblock(tsc_ctx* ctx, int32_t dtype, const void* x, const int32_t* nbr,
 
 /* ---- per-voxel linear layer ---------------------------------------------------------------- */
 /* out (N,Cout) = x (N,Cin) * weight^T + bias (+ residual); weight (Cout,Cin) as nn.Linear, bias
- * (Cout) or NULL, residual (N,Cout) or NULL (it may alias out; x may not).  All `dtype`, fp32
+ * (Cout) or NULL, residual (N,Cout) or NULL (it may be out itself; any other overlap of out with
+ * residual or with x is TSC_ERR_INVALID).  All `dtype`, fp32
  * accumulation, one hipBLASLt GEMM (bias epilogue, residual as its C operand).  The first call
  * of a shape on a context times the library's candidate algorithms (into scratch rows, so an
  * in-place residual is not applied twice) and synchronizes the stream once; later calls only

@@ -179,3 +179,26 @@ def test_map_rejects_bad_arguments(pkg, dev):
         pkg.build_neighbor_map(c, (4, 4, 4), 1, dilation=(0, 1, 1))
     with pytest.raises(pkg.TscError):
         pkg.build_neighbor_map(c[:, 1:].contiguous(), (4, 4, 4), 1)
+
+
+@pytest.mark.parametrize("n", [1, 111, 113, 100003])
+def test_write_floor_writes_the_fill_pattern(pkg, dev, n):
+    """tsc_map_write_floor (the measurement kernel bench.py times beside the fill): every row
+    rows[i] comes out as (-1, row, -1) x 9, through a permutation and with rows NULL (i); rows of
+    the table it is not given stay untouched."""
+    import ctypes
+
+    ctx = pkg._lib.context(dev.index)
+    perm = torch.randperm(n, generator=torch.Generator().manual_seed(n)).to(torch.int32).to(dev)
+    want = torch.tensor([-1, 0, -1] * 9, dtype=torch.int32).repeat(n, 1)
+    want[:, 1::3] = torch.arange(n, dtype=torch.int32)[:, None]
+    print(f"  write floor n={n}", flush=True)
+    for rows in (perm, None):
+        out = torch.full((n + 1, 27), 7, dtype=torch.int32, device=dev)  # one row past the table
+        st = ctx.lib.tsc_map_write_floor(ctx.bind(), None if rows is None else
+                                         ctypes.c_void_p(rows.data_ptr()), n,
+                                         ctypes.c_void_p(out.data_ptr()))
+        assert st == 0, ctx.lib.tsc_last_error()
+        got = out.cpu()
+        assert torch.equal(got[:n], want)
+        assert (got[n] == 7).all()

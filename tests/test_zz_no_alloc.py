@@ -74,6 +74,53 @@ def test_noalloc_matches_conv_fused(pkg, dev, dtype, ci, co, epi):
             assert torch.equal(r2, want)
 
 
+def test_noalloc_first_call_on_fresh_context_under_graph_capture(pkg, dev):
+    """'Allocates nothing', checked by behaviour: the first call on a new context, whose
+    workspaces are all empty, is captured into a CUDA (HIP) graph.  During a capture any
+    hipMalloc, hipFree or stream synchronization (what growing a workspace does) fails the call and
+    the capture, so a path that reached for the context's workspace would not pass.  The graph is
+    replayed three times with eager calls on other inputs in between; every replay must equal
+    tsc_conv_fused bit for bit.  The captured kernels write no memset node (the schedule is built
+    by kernels).  bf16 256->256 uses the 256-row tiles and their longest-first schedule."""
+    coords = pkg.workloads.make_coords("resblock64_bf16")
+    m, f, w, b, r, g = _inputs(pkg, dev, coords, 256, 256, torch.bfloat16, 3)
+    order = m.conv_order()
+    n = len(coords)
+    want = _run(pkg, "tsc_conv_fused", f, w, b, m.nbr, order, "bias", None, None,
+                torch.empty((n, 256), dtype=torch.bfloat16, device=dev))
+    # The device's scratch address is looked up once per device; do it outside the capture, on
+    # the shared context (not the fresh one).
+    _run(pkg, "tsc_conv_fused_noalloc", f, w, b, m.nbr, order, "bias", None, None,
+         torch.empty((n, 256), dtype=torch.bfloat16, device=dev))
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream(dev)
+    with torch.cuda.stream(side):
+        fresh = pkg._lib.Context(dev.index)  # bound to the capture stream from the start
+    out = torch.full((n, 256), float("nan"), dtype=torch.bfloat16, device=dev)
+    graph = torch.cuda.CUDAGraph()
+    print(f"  noalloc under graph capture N={n}", flush=True)
+    with torch.cuda.graph(graph, stream=side):
+        st = fresh.lib.tsc_conv_fused_noalloc(
+            fresh.bind(), _CODES[torch.bfloat16], _p(f), _p(w), _p(b), _p(m.nbr), _p(order), n,
+            256, 256, _EPI["bias"], None, None, None, ctypes.c_float(1e-6), _p(out))
+    assert st == 0, fresh.lib.tsc_last_error().decode()
+    try:
+        small = coords[coords[:, 0] == 0][:5000].copy()
+        for i in range(3):
+            out.fill_(float("nan"))
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, want), f"replay {i}"
+            # eager work in between: another shape through the shared context
+            m2, f2, w2, b2, _, _ = _inputs(pkg, dev, small, 256, 256, torch.bfloat16, 10 + i)
+            _run(pkg, "tsc_conv_fused_noalloc", f2, w2, b2, m2.nbr, m2.conv_order(), "bias", None,
+                 None, torch.empty((len(small), 256), dtype=torch.bfloat16, device=dev))
+            torch.cuda.synchronize()
+    finally:
+        del graph
+        fresh.lib.tsc_ctx_destroy(fresh.handle)
+
+
 def test_noalloc_rejects_rows_beyond_scratch(pkg, dev):
     """N above 65536 tiles of 256 rows is refused before any launch (small dummy buffers)."""
     ctx = pkg._lib.context(dev.index)

@@ -60,6 +60,7 @@ _SIGNATURES = {
     "tsc_memset_zero": (_I32, [_P, _P, _SZ]),
     "tsc_map_key_bytes": (_I32, [_I32, _I32, _I32, _I32]),
     "tsc_map_build": (_I32, [_P, _P, _I64, _I32, _I32, _I32, _I32, _P, _P, _I32, _P, _P, _P, _P]),
+    "tsc_map_write_floor": (_I32, [_P, _P, _I64, _P]),
     "tsc_map_conv_order": (_I32, [_P, _P, _P, _I64, _P]),
     "tsc_map_gather_plan_bytes": (_I64, [_I64]),
     "tsc_map_gather_plan": (_I32, [_P, _P, _P, _I64, _I32, _I32, _I32, _I32, _P]),

@@ -63,8 +63,36 @@ int workspace(tsc_ctx* ctx, size_t bytes, void** out) {
   return grow_buffer(ctx, &ctx->ws, &ctx->ws_bytes, bytes, "workspace", out);
 }
 
-int sched_workspace(tsc_ctx* ctx, size_t bytes, void** out) {
-  return grow_buffer(ctx, &ctx->ws_sched, &ctx->ws_sched_bytes, bytes, "schedule workspace", out);
+int sched_cached(tsc_ctx* ctx, const int32_t* nbr, const int32_t* order, int64_t N, int32_t bm,
+                 size_t bytes, tsc_sched_entry** entry) {
+  const uint64_t now = ++ctx->sched_tick;
+  for (auto& e : ctx->sched)
+    if (e.valid && e.nbr == nbr && e.order == order && e.N == N && e.bm == bm && e.bytes >= bytes) {
+      e.used = now;
+      *entry = &e;
+      return TSC_OK;
+    }
+  if ((int)ctx->sched.size() < kSchedCacheEntries) ctx->sched.emplace_back();
+  tsc_sched_entry* victim = &ctx->sched[0];
+  for (auto& e : ctx->sched)
+    if (e.used < victim->used) victim = &e;
+  victim->valid = false;
+  void* buf;
+  const int st = grow_buffer(ctx, &victim->buf, &victim->bytes, bytes, "schedule workspace", &buf);
+  if (st) return st;
+  victim->nbr = nbr;
+  victim->order = order;
+  victim->N = N;
+  victim->bm = bm;
+  victim->used = now;
+  *entry = victim;
+  return TSC_OK;
+}
+
+void sched_forget(tsc_ctx* ctx, const void* p) {
+  if (!p) return;
+  for (auto& e : ctx->sched)
+    if ((const void*)e.nbr == p || (const void*)e.order == p) e.valid = false;
 }
 
 int blas_workspace(tsc_ctx* ctx, size_t bytes, void** out) {
@@ -80,6 +108,12 @@ void prof_clear(tsc_ctx* ctx) {
 }
 
 static bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+// True when the byte ranges [a, a + na) and [b, b + nb) share a byte.
+static bool overlaps(const void* a, size_t na, const void* b, size_t nb) {
+  const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
+  return na && nb && x < y + nb && y < x + na;
+}
 
 static int elem_size(int32_t dtype) {
   switch (dtype) {
@@ -157,14 +191,8 @@ int tsc_ctx_create(int device, void* stream, tsc_ctx** out) {
   if (st) return st;
   if (device < 0 || device >= ndev)
     return fail(TSC_ERR_INVALID, "ctx_create: device %d not in [0,%d)", device, ndev);
-  DeviceGuard g(device);
-  // The device's static schedule scratch (tsc_conv_fused_noalloc), looked up while it is current.
-  void* scratch_dev = nullptr;
-  st = sched_scratch_ptr(device, &scratch_dev);
-  if (st) return st;
   tsc_ctx* c = new tsc_ctx();
   c->device = device;
-  c->sched_scratch = scratch_dev;
   c->ws = nullptr;
   c->ws_bytes = 0;
   c->stream = (hipStream_t)stream;  // NULL = the HIP null stream
@@ -178,7 +206,8 @@ int tsc_ctx_destroy(tsc_ctx* ctx) {
   DeviceGuard g(ctx->device);
   int st = check_hip(hipStreamSynchronize(ctx->stream), "ctx_destroy sync");
   if (ctx->ws) (void)hipFree(ctx->ws);
-  if (ctx->ws_sched) (void)hipFree(ctx->ws_sched);
+  for (auto& e : ctx->sched)
+    if (e.buf) (void)hipFree(e.buf);
   blas_destroy(ctx);
   if (ctx->ws_blas) (void)hipFree(ctx->ws_blas);
   st_release(ctx);
@@ -233,6 +262,7 @@ int tsc_free(tsc_ctx* ctx, void* ptr) {
   DeviceGuard g(ctx->device);
   st = check_hip(hipStreamSynchronize(ctx->stream), "free sync");
   if (st) return st;
+  sched_forget(ctx, ptr);
   return check_hip(hipFree(ptr), "hipFree");
 }
 
@@ -313,11 +343,26 @@ int tsc_map_build(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t B, int
     return fail(TSC_ERR_UNSUPPORTED, "map_build: grid of %lld cells too large for the bitmap path",
                 (long long)cells);
   DeviceGuard g(ctx->device);
+  sched_forget(ctx, nbr_out);
   if (method == TSC_MAP_RADIX)
     return map_build_radix(ctx, coords, N, B, X, Y, Z, dilation, keys_out, perm_out, nbr_out,
                            status_dev);
   return map_build_bitmap(ctx, coords, N, B, X, Y, Z, dilation, keys_out, perm_out, nbr_out,
                           status_dev);
+}
+
+int tsc_map_write_floor(tsc_ctx* ctx, const int32_t* rows, int64_t N, int32_t* out) {
+  g_err[0] = 0;
+  int st = check_ctx(ctx);
+  if (st) return st;
+  if (N < 0 || N > INT32_MAX)
+    return fail(TSC_ERR_INVALID, "map_write_floor: N=%lld out of range", (long long)N);
+  if (N > 0 && !out) return fail(TSC_ERR_INVALID, "map_write_floor: null out");
+  if (!aligned(out, 4) || !aligned(rows, 4))
+    return fail(TSC_ERR_INVALID, "map_write_floor: rows and out must be 4-byte aligned");
+  DeviceGuard g(ctx->device);
+  sched_forget(ctx, out);
+  return tsc::map_write_floor_launch(ctx, rows, N, out);
 }
 
 int tsc_map_conv_order(tsc_ctx* ctx, const int32_t* nbr, const int32_t* perm, int64_t N,
@@ -329,6 +374,7 @@ int tsc_map_conv_order(tsc_ctx* ctx, const int32_t* nbr, const int32_t* perm, in
     return fail(TSC_ERR_INVALID, "map_conv_order: N=%lld out of range", (long long)N);
   if (N > 0 && (!nbr || !order_out)) return fail(TSC_ERR_INVALID, "map_conv_order: null nbr/order");
   DeviceGuard g(ctx->device);
+  sched_forget(ctx, order_out);
   return tsc::conv_order_launch(ctx, nbr, perm, N, order_out);
 }
 
@@ -444,8 +490,10 @@ int tsc_conv_fused_noalloc(tsc_ctx* ctx, int32_t dtype, const void* feats, const
     return fail(TSC_ERR_INVALID, "conv_noalloc: N=%lld exceeds the static scratch limit of %lld "
                                  "rows", (long long)N, (long long)kNoallocMaxRows);
   if (N == 0) return TSC_OK;
-  if (!ctx->sched_scratch) return fail(TSC_ERR_HIP, "conv_noalloc: no scratch for this device");
   DeviceGuard g(ctx->device);
+  // This device's static scratch: looked up (hipGetSymbolAddress, once per device, cached) by the
+  // first call on the context, with the device current.
+  if (!ctx->sched_scratch && (st = sched_scratch_ptr(ctx->device, &ctx->sched_scratch))) return st;
   // Per-kernel profiling records events (an allocation): off for this call.
   const bool prof = ctx->profile;
   ctx->profile = false;
@@ -511,7 +559,9 @@ int tsc_resblock(tsc_ctx* ctx, int32_t dtype, const void* x, const int32_t* nbr,
       (ln_beta && !aligned(ln_beta, es)))
     return fail(TSC_ERR_INVALID, "resblock: w2, b2, ln_gamma and ln_beta must be aligned to "
                                  "their element size");
-  if (x == out) return fail(TSC_ERR_INVALID, "resblock: out must not alias x");
+  const size_t rows_bytes = (size_t)N * C * es;
+  if (overlaps(x, rows_bytes, out, rows_bytes))
+    return fail(TSC_ERR_INVALID, "resblock: out must not overlap x");
   DeviceGuard g(ctx->device);
   void* h;
   st = workspace(ctx, (size_t)N * C * elem_size(dtype), &h);
@@ -536,7 +586,12 @@ int tsc_linear(tsc_ctx* ctx, int32_t dtype, const void* x, int64_t N, int32_t Ci
   if (N < 0 || Cin <= 0 || Cout <= 0)
     return fail(TSC_ERR_INVALID, "linear: bad shape N=%lld Cin=%d Cout=%d", (long long)N, Cin, Cout);
   if (N > 0 && (!x || !weight || !out)) return fail(TSC_ERR_INVALID, "linear: null buffer");
-  if (x == out) return fail(TSC_ERR_INVALID, "linear: out must not alias x");
+  const size_t es = (size_t)elem_size(dtype);
+  const size_t out_bytes = (size_t)N * Cout * es;
+  if (overlaps(x, (size_t)N * Cin * es, out, out_bytes))
+    return fail(TSC_ERR_INVALID, "linear: out must not overlap x");
+  if (residual && residual != out && overlaps(residual, out_bytes, out, out_bytes))
+    return fail(TSC_ERR_INVALID, "linear: residual must be out itself or not overlap it");
   DeviceGuard g(ctx->device);
   return linear_launch(ctx, dtype, x, N, Cin, weight, bias, residual, Cout, out);
 }

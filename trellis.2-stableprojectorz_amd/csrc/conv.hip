@@ -829,25 +829,33 @@ int launch_cfg(tsc_ctx* ctx, const ConvArgs& a) {
     const int32_t lists = 8, per_list = (m_tiles + lists - 1) / lists;
     const size_t need = ((size_t)m_tiles + (size_t)lists * per_list) * 4;
     void* ws;
-    if (a.sched_scratch) {  // the caller's fixed buffer (tsc_conv_fused_noalloc)
+    tsc_sched_entry* entry = nullptr;
+    if (a.sched_scratch) {  // the caller's fixed buffer (tsc_conv_fused_noalloc): built per call
       if (need > a.sched_scratch_bytes)
         return fail(TSC_ERR_INVALID, "conv: schedule needs %zu bytes of scratch, %zu available",
                     need, a.sched_scratch_bytes);
       ws = a.sched_scratch;
-    } else {
-      int st = sched_workspace(ctx, need, &ws);
+    } else {  // the context's cache: built by the first conv over this map and row order
+      int st = sched_cached(ctx, a.nbr, a.order, a.N, BM, need, &entry);
       if (st) return st;
+      ws = entry->buf;
     }
     int32_t* cost = (int32_t*)ws;
     int32_t* map = cost + m_tiles;
-    {
-      ProfScope p(ctx, "conv_tile_cost");
-      tile_cost_kernel<<<m_tiles, kSchedThreads, 0, ctx->stream>>>(a.nbr, a.order, a.N, BM, cost);
-    }
-    {
-      ProfScope p(ctx, "conv_tile_schedule");
-      tile_schedule_kernel<<<1, kSchedThreads, 0, ctx->stream>>>(cost, m_tiles, lists, per_list,
-                                                                   map);
+    if (!entry || !entry->valid) {
+      {
+        ProfScope p(ctx, "conv_tile_cost");
+        tile_cost_kernel<<<m_tiles, kSchedThreads, 0, ctx->stream>>>(a.nbr, a.order, a.N, BM,
+                                                                       cost);
+      }
+      {
+        ProfScope p(ctx, "conv_tile_schedule");
+        tile_schedule_kernel<<<1, kSchedThreads, 0, ctx->stream>>>(cost, m_tiles, lists,
+                                                                     per_list, map);
+      }
+      int st = check_hip(hipGetLastError(), "conv tile schedule");
+      if (st) return st;
+      if (entry) entry->valid = true;
     }
     tile_map = map;
     per_xcd = per_list * n_tiles;

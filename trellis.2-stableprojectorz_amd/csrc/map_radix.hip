@@ -1372,6 +1372,49 @@ int morton_impl(tsc_ctx* ctx, const int32_t* coords, int64_t N, int bits, int sh
 
 }  // namespace
 
+namespace {
+
+// The store side of fill_window_kernel alone (a measurement kernel; no product path runs it): the
+// same blocks of 112 consecutive sorted voxels dealt to the XCDs in contiguous runs, the same
+// 7 voxels per wave over 4 rounds, and the same 9 lanes x 12 bytes of each voxel's 108-byte row
+// at its original row rows[i] (i when rows is null).  rows[i] is its only load, so its time is
+// what the fill would take if its window copies and searches cost nothing: the floor of a table
+// laid out in the caller's row order.  The words written are (-1, row, -1) per lane.
+__global__ void __launch_bounds__(kFillThreads)
+    write_floor_kernel(const int32_t* __restrict__ rows, int64_t n, int32_t per_xcd,
+                       int32_t* __restrict__ out) {
+  constexpr int VOX = kFillRounds * mapk::kFillVoxPerWave * (kFillThreads / 64);
+  const int64_t i0 = ((int64_t)(blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3)) * VOX;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int slot = lane / mapk::kFillLanes, col = lane - slot * mapk::kFillLanes;
+  if (slot >= mapk::kFillVoxPerWave) return;
+  const int li0 = wid * kFillRounds * mapk::kFillVoxPerWave + slot;
+#pragma unroll
+  for (int r = 0; r < kFillRounds; ++r) {
+    const int64_t i = i0 + li0 + r * mapk::kFillVoxPerWave;
+    if (i >= n) break;
+    const int32_t row = rows ? rows[i] : (int32_t)i;
+    if (row < 0 || row >= n) continue;
+    int32_t* dst = out + (int64_t)row * 27 + col * 3;
+    dst[0] = -1;
+    dst[1] = row;
+    dst[2] = -1;
+  }
+}
+
+}  // namespace
+
+int map_write_floor_launch(tsc_ctx* ctx, const int32_t* rows, int64_t N, int32_t* out) {
+  if (N == 0) return TSC_OK;
+  constexpr int VOX = kFillRounds * mapk::kFillVoxPerWave * (kFillThreads / 64);
+  const int64_t blocks = (N + VOX - 1) / VOX;
+  const int32_t per_xcd = (int32_t)((blocks + 7) / 8);
+  ProfScope ps(ctx, "map_write_floor");
+  write_floor_kernel<<<(unsigned)per_xcd * 8u, kFillThreads, 0, ctx->stream>>>(rows, N, per_xcd,
+                                                                               out);
+  return check_hip(hipGetLastError(), "map_write_floor launch");
+}
+
 int sort_rows_morton(tsc_ctx* ctx, const int32_t* coords, int64_t N, int bits, int shift,
                      int nbits, int32_t* rows_out) {
   if (N == 0) return TSC_OK;

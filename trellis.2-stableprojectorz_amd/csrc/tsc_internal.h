@@ -21,16 +21,33 @@ struct tsc_prof_agg {
   int64_t launches;
 };
 
+// A longest-first tile schedule of the 256-row conv tiles (conv.hip) kept for reuse.  It depends
+// only on the neighbor map, the row order, N and the tile height, so every conv over one
+// coordinate set (the eight convs of a ResBlock chain) builds it once.  Keyed by the buffers'
+// addresses: an entry is dropped when tsc_map_build or tsc_map_conv_order writes to, or tsc_free
+// releases, one of them.  Whatever a stale entry holds, it is a permutation of the same tiles, so
+// it can only change which block computes a tile, never a result.
+struct tsc_sched_entry {
+  const int32_t* nbr = nullptr;
+  const int32_t* order = nullptr;
+  int64_t N = -1;
+  int32_t bm = 0;
+  bool valid = false;   // schedule written (launched) for this key
+  void* buf = nullptr;  // device: cost per tile, then the XCD lists
+  size_t bytes = 0;
+  uint64_t used = 0;    // last use, for replacement
+};
+
 struct tsc_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
   // Growable device workspace (stream-ordered users; grown only after a stream sync).
   void* ws = nullptr;
   size_t ws_bytes = 0;
-  // Second growable buffer for the conv tile schedule (a conv may run while `ws` holds the
-  // intermediate rows of a ResBlock).
-  void* ws_sched = nullptr;
-  size_t ws_sched_bytes = 0;
+  // Cached conv tile schedules (a conv may run while `ws` holds the intermediate rows of a
+  // ResBlock, so they live in buffers of their own).
+  std::vector<tsc_sched_entry> sched;
+  uint64_t sched_tick = 0;
   // hipBLASLt handle (created on the first linear layer) and its workspace.
   void* blaslt = nullptr;
   void* ws_blas = nullptr;
@@ -41,7 +58,8 @@ struct tsc_ctx {
   hipEvent_t st_ev[2] = {nullptr, nullptr};
   bool st_pending[2] = {false, false};
   int st_next = 0;  // chunk the next load starts with
-  // Device address of this device's static schedule scratch (tsc_conv_fused_noalloc).
+  // Device address of this device's static schedule scratch, looked up by the first
+  // tsc_conv_fused_noalloc call on this context.
   void* sched_scratch = nullptr;
   bool profile = false;
   std::vector<tsc_prof_rec> prof;      // pending launches
@@ -56,9 +74,17 @@ int check_hip(hipError_t e, const char* what);
 
 // Ensures ctx->ws holds at least `bytes`; returns TSC_OK or an error status.
 int workspace(tsc_ctx* ctx, size_t bytes, void** out);
-// The same for ctx->ws_sched and ctx->ws_blas.
-int sched_workspace(tsc_ctx* ctx, size_t bytes, void** out);
+// The same for ctx->ws_blas.
 int blas_workspace(tsc_ctx* ctx, size_t bytes, void** out);
+// The cached tile schedule of (nbr, order, N, bm).  On a hit *entry->valid is true and
+// entry->buf holds it; on a miss the least recently used entry (at most kSchedCacheEntries) is
+// re-keyed with valid = false and its buffer grown to `bytes`; the caller launches the schedule
+// kernels into it and then sets valid.
+constexpr int kSchedCacheEntries = 4;
+int sched_cached(tsc_ctx* ctx, const int32_t* nbr, const int32_t* order, int64_t N, int32_t bm,
+                 size_t bytes, tsc_sched_entry** entry);
+// Drops the cached schedules whose neighbor map or row order is the buffer at p.
+void sched_forget(tsc_ctx* ctx, const void* p);
 
 void prof_clear(tsc_ctx* ctx);
 
@@ -104,6 +130,11 @@ int map_build_radix(tsc_ctx* ctx, const int32_t* coords, int64_t N, int32_t B, i
 // of map_build_radix with a Morton key.  Writes rows_out[0..N).
 int sort_rows_morton(tsc_ctx* ctx, const int32_t* coords, int64_t N, int bits, int shift,
                      int nbits, int32_t* rows_out);
+
+// The store pattern of the radix path's fill alone (a measurement kernel): row rows[i] (i when
+// rows is null) of the (N,27) int32 table `out` written as the fill writes it; rows outside
+// [0, N) are skipped.
+int map_write_floor_launch(tsc_ctx* ctx, const int32_t* rows, int64_t N, int32_t* out);
 
 // ---- launcher implemented in conv_order.hip ----
 int conv_order_launch(tsc_ctx* ctx, const int32_t* nbr, const int32_t* perm, int64_t N,
