@@ -142,7 +142,7 @@ def test_native_header_edge_cases(pkg, tmp_path):
 @pytest.mark.parametrize("case", [
     "short", "len_too_big", "not_json", "unknown_dtype", "offsets_past_end", "size_mismatch",
     "duplicate", "trailing", "metadata_not_string", "missing_shape", "negative_dim",
-    "float_offsets"])
+    "float_offsets", "lone_low_surrogate", "raw_control_char", "invalid_utf8"])
 def test_native_header_rejects(pkg, tmp_path, case):
     p = tmp_path / "bad.safetensors"
     ok = {"t": {"dtype": "F32", "shape": [2], "data_offsets": [0, 8]}}
@@ -171,9 +171,29 @@ def test_native_header_rejects(pkg, tmp_path, case):
         _write(p, {"t": {"dtype": "F32", "shape": [-2], "data_offsets": [0, 8]}}, bytes(8))
     elif case == "float_offsets":
         _write(p, {"t": {"dtype": "F32", "shape": [2], "data_offsets": [0, 8.0]}}, bytes(8))
+    elif case in STRING_CASES:
+        _write_raw(p, STRING_CASES[case], 1)
     with pytest.raises(pkg.TscError) as ei:
         _native_header(pkg, p)
     assert ei.value.status == 1, str(ei.value)
+    if case in STRING_CASES:  # the safetensors package refuses these headers too
+        from safetensors.numpy import load_file
+        with pytest.raises(Exception):
+            load_file(str(p))
+
+
+# Tensor names the safetensors package's JSON reader refuses: a \u escape of a low surrogate with
+# no high surrogate before it, an unescaped control byte, and bytes that are not UTF-8.
+STRING_CASES = {
+    "lone_low_surrogate": b'{"\\udc00": {"dtype": "U8", "shape": [1], "data_offsets": [0, 1]}}',
+    "raw_control_char": b'{"a\x01b": {"dtype": "U8", "shape": [1], "data_offsets": [0, 1]}}',
+    "invalid_utf8": b'{"a\xffb": {"dtype": "U8", "shape": [1], "data_offsets": [0, 1]}}',
+}
+
+
+def _write_raw(path, header: bytes, data_len: int):
+    path.write_bytes(struct.pack("<Q", len(header)) + header + bytes(data_len))
+    return path
 
 
 def test_native_missing_file_and_unknown_tensor(pkg, tmp_path):

@@ -70,8 +70,16 @@ def _corpus(d: Path) -> list:
         ("deep", "[" * 200 + "]" * 200, b""),
         ("lone_surrogate", '{"\\ud800": {"dtype": "U8", "shape": [1], "data_offsets": [0, 1]}}',
          bytes(1)),
+        ("lone_low_surrogate", '{"\\udc00": {"dtype": "U8", "shape": [1], "data_offsets": [0, 1]}}',
+         bytes(1)),
+        ("raw_control_char", '{"a\x01b": {"dtype": "U8", "shape": [1], "data_offsets": [0, 1]}}',
+         bytes(1)),
     ]:
         files.append(_write(d / f"{name}.safetensors", hdr, data))
+    p = d / "invalid_utf8.safetensors"
+    hb = b'{"a\xffb": {"dtype": "U8", "shape": [1], "data_offsets": [0, 1]}}'
+    p.write_bytes(struct.pack("<Q", len(hb)) + hb + bytes(1))
+    files.append(p)
     return files
 
 

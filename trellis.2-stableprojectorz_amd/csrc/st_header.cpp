@@ -14,6 +14,32 @@
 namespace tsc {
 namespace {
 
+// True when [s, s + n) is well-formed UTF-8 (RFC 3629: no overlong forms, no surrogates, nothing
+// past U+10FFFF).  The reference format's reader decodes the header as UTF-8 text before it parses
+// the JSON, so a header that is not UTF-8 is rejected as a whole.
+bool valid_utf8(const char* s, size_t n) {
+  const unsigned char* u = (const unsigned char*)s;
+  size_t i = 0;
+  while (i < n) {
+    const unsigned c = u[i];
+    if (c < 0x80) { ++i; continue; }
+    int len;
+    unsigned cp, min;
+    if ((c & 0xE0) == 0xC0) { len = 2; cp = c & 0x1F; min = 0x80; }
+    else if ((c & 0xF0) == 0xE0) { len = 3; cp = c & 0x0F; min = 0x800; }
+    else if ((c & 0xF8) == 0xF0) { len = 4; cp = c & 0x07; min = 0x10000; }
+    else return false;
+    if (n - i < (size_t)len) return false;
+    for (int k = 1; k < len; ++k) {
+      if ((u[i + k] & 0xC0) != 0x80) return false;
+      cp = (cp << 6) | (u[i + k] & 0x3F);
+    }
+    if (cp < min || cp > 0x10FFFF || (cp >= 0xD800 && cp < 0xE000)) return false;
+    i += (size_t)len;
+  }
+  return true;
+}
+
 struct Json {
   const char* start;
   const char* p;
@@ -70,6 +96,7 @@ struct Json {
     out->clear();
     while (p < end && *p != '"') {
       const char c = *p++;
+      if ((unsigned char)c < 0x20) { err = "control character in a string"; return false; }
       if (c != '\\') {
         out->push_back(c);
         continue;
@@ -88,6 +115,7 @@ struct Json {
         case 'u': {
           unsigned v;
           if (!hex4(&v)) { err = "bad \\u escape"; return false; }
+          if (v >= 0xDC00 && v < 0xE000) { err = "lone low surrogate"; return false; }
           if (v >= 0xD800 && v < 0xDC00) {  // surrogate pair
             unsigned lo;
             if (end - p < 6 || p[0] != '\\' || p[1] != 'u') { err = "lone surrogate"; return false; }
@@ -201,6 +229,7 @@ bool st_parse_header(tsc_st* f, const char* text, size_t len, std::string* err) 
     *err = what;
     return false;
   };
+  if (!valid_utf8(text, len)) return bad("header is not UTF-8");
   if (!j.expect('{')) return bad(j.err);
   if (j.peek('}')) {
     ++j.p;
