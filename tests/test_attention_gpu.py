@@ -149,3 +149,30 @@ def test_attention_rejects_bad_arguments(pkg, dev):
         pkg.sparse_attention(y, y, y, [0, 10])            # head_dim 96
     with pytest.raises(pkg.TscError):
         pkg.sparse_attention(x, x.float(), x, [0, 10])    # mixed dtypes
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_device_cu_seqlens_make_no_host_read(pkg, dev, dtype):
+    """Device cu_seqlens go to the kernel as given: under torch's sync debug mode "error" (any
+    device-to-host read raises) the call succeeds, and the result equals the call with host
+    offsets bit for bit.  The sequences are unbalanced (one 6x the mean), so the default grid size
+    (twice the mean length) leaves the longest one to the kernel's tile loop; empty and 1-row
+    sequences included.  Rows outside every sequence come out zero."""
+    rng = np.random.default_rng(21)
+    cu = [3, 3, 4, 130, 3130, 3200, 3456]
+    tq, h, d = 3470, 4, 128
+    q, k, v = _inputs(rng, tq, tq, h, d, dtype)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    cu_dev = torch.tensor(cu, dtype=torch.int32, device=dev)
+    print(f"  attention device cu_seqlens {dtype}", flush=True)
+    want = pkg.sparse_attention(qd, kd, vd, cu)
+    torch.cuda.synchronize()
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        got = pkg.sparse_attention(qd, kd, vd, cu_dev)
+    finally:
+        torch.cuda.set_sync_debug_mode(0)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    assert not got[:3].any() and not got[3456:].any()
+    _check(got, q, k, v, cu, cu, dtype)

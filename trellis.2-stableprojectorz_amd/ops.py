@@ -334,33 +334,42 @@ def sparse_linear(x: torch.Tensor, weight: torch.Tensor, bias=None, residual=Non
 
 
 def _cu_seqlens(cu, total: int, dev: int, what: str):
-    """cu_seqlens as (host int64 array, device int32 tensor), checked non-decreasing in [0, total]."""
+    """cu_seqlens as (host int64 array or None, device int32 tensor).
+
+    A host sequence is checked non-decreasing within [0, total] and copied to the device.  A
+    device tensor is taken as given (host None): reading it would synchronize the stream, and the
+    kernels clamp every offset into [0, total], so a malformed array cannot read out of bounds."""
     import numpy as np
 
-    if isinstance(cu, torch.Tensor):
-        host = cu.detach().to("cpu", torch.int64).numpy()
-    else:
-        host = np.asarray(cu, np.int64)
+    if isinstance(cu, torch.Tensor) and cu.is_cuda:
+        if cu.dim() != 1 or cu.numel() < 1:
+            raise TscError(_lib.TSC_ERR_INVALID, f"{what} must be a 1-D (B+1,) sequence")
+        d = cu if cu.dtype == torch.int32 and cu.is_contiguous() else cu.to(torch.int32).contiguous()
+        return None, d
+    host = (cu.detach().to("cpu", torch.int64).numpy() if isinstance(cu, torch.Tensor)
+            else np.asarray(cu, np.int64))
     if host.ndim != 1 or host.size < 1:
         raise TscError(_lib.TSC_ERR_INVALID, f"{what} must be a 1-D (B+1,) sequence")
     if (np.diff(host) < 0).any() or host[0] < 0 or host[-1] > total:
         raise TscError(_lib.TSC_ERR_INVALID, f"{what} must be non-decreasing within [0, {total}]")
-    if isinstance(cu, torch.Tensor) and cu.is_cuda and cu.dtype == torch.int32 and cu.is_contiguous():
-        d = cu
-    else:
-        d = torch.from_numpy(host.astype(np.int32)).to(f"cuda:{dev}")
-    return host, d
+    return host, torch.from_numpy(host.astype(np.int32)).to(f"cuda:{dev}")
 
 
 def sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens_q,
                      cu_seqlens_kv=None, num_heads: int | None = None, head_dim: int | None = None,
-                     scale: float | None = None, out=None) -> torch.Tensor:
+                     scale: float | None = None, out=None,
+                     max_seqlen_q: int | None = None) -> torch.Tensor:
     """sparseAttention (src/sparse/ops/attention.ts:24-79) on the GPU for any batch size.
 
     q (total_q, H, D) and k / v (total_kv, H, D), or (total, H*D) with num_heads; cu_seqlens_q /
     cu_seqlens_kv (B+1,) row offsets of each sequence (host sequence or tensor; cu_seqlens_kv
     defaults to cu_seqlens_q).  Returns (total_q, H, D) in q's dtype.  scale defaults to
-    1/sqrt(D).  One tsc_attention call; no host round trip."""
+    1/sqrt(D).  One tsc_attention call; no host round trip: device cu_seqlens are never read on
+    the host (they are not validated there; the kernel clamps them), and then max_seqlen_q, which
+    only sizes the grid, defaults to min(total_q, 2 * ceil(total_q / B)) — every query is covered
+    whatever its sequence's length, longer ones at a lower parallelism.  Rows of a new `out`
+    outside every query sequence are zero, as in the reference's zero-initialised output
+    (attention.ts:49)."""
     dev = _dev(q, k, v, out)
     if q.dim() == 2:
         if not num_heads:
@@ -379,21 +388,25 @@ def sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqle
     cq_host, cq = _cu_seqlens(cu_seqlens_q, tq, dev, "cu_seqlens_q")
     if cu_seqlens_kv is None:
         cu_seqlens_kv = cu_seqlens_q
-    ck_host, ck = _cu_seqlens(cu_seqlens_kv, tkv, dev, "cu_seqlens_kv")
-    if len(ck_host) != len(cq_host):
+    _, ck = _cu_seqlens(cu_seqlens_kv, tkv, dev, "cu_seqlens_kv")
+    if ck.numel() != cq.numel():
         raise TscError(_lib.TSC_ERR_INVALID, "cu_seqlens_q and cu_seqlens_kv differ in length")
-    b = len(cq_host) - 1
+    b = cq.numel() - 1
     if out is None:
-        # rows outside every sequence stay zero, as in the reference's zero-initialised output
-        # (attention.ts:49); the kernel writes every row inside one
-        covered = b > 0 and cq_host[0] == 0 and cq_host[-1] == tq
+        # the kernel writes every row inside a query sequence; zero-fill unless they cover all
+        covered = cq_host is not None and b > 0 and cq_host[0] == 0 and cq_host[-1] == tq
         out = (torch.empty if covered else torch.zeros)((tq, h, d), dtype=q.dtype, device=q.device)
     elif out.numel() != tq * h * d or out.dtype != q.dtype:
         raise TscError(_lib.TSC_ERR_INVALID, "out has the wrong size or dtype")
-    max_q = int((cq_host[1:] - cq_host[:-1]).max()) if b > 0 else 0
+    if max_seqlen_q is None:
+        if cq_host is not None:
+            max_seqlen_q = int((cq_host[1:] - cq_host[:-1]).max()) if b > 0 else 0
+        else:
+            max_seqlen_q = min(tq, 2 * -(-tq // b)) if b > 0 else 0
     ctx = _lib.context(dev)
     check(ctx.lib.tsc_attention(ctx.bind(), _code(q), _p(q), _p(k), _p(v), _p(cq), _p(ck), b, tq,
-                                tkv, h, d, float(scale) if scale else 0.0, max_q, _p(out)))
+                                tkv, h, d, float(scale) if scale else 0.0, int(max_seqlen_q),
+                                _p(out)))
     return out.view(tq, h, d)
 
 
