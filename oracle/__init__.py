@@ -208,18 +208,22 @@ def linear(x, weight, bias=None, residual=None) -> np.ndarray:
     return y
 
 
-def convnext_block(feats, nbr, conv_w, conv_b, w0, b0, w2, b2, eps=1e-6, rows=None):
+def convnext_block(feats, nbr, conv_w, conv_b, w0, b0, w2, b2, eps=1e-6, rows=None, store=None):
     """Sparse ConvNeXt block (src/models/sparse_unet_vae_decoder.ts:48-78), fp64:
     h = conv(x); h = LN(h); h = h W0^T + b0; h = silu(LN(h)); out = x + h W2^T + b2.
-    rows: optional subset of output rows (the conv reads neighbors from all of feats)."""
+    rows: optional subset of output rows (the conv reads neighbors from all of feats).
+    store: optional rounding (fp64 array -> fp64 array of representable values) applied where the
+    TS block stores a step's tensor in its storage type: after the conv, the first LayerNorm, the
+    first linear, the LayerNorm + SiLU and the output."""
+    st = (lambda a: a) if store is None else store
     f = np.asarray(feats, np.float64)
     nb = np.asarray(nbr) if rows is None else np.asarray(nbr)[rows]
-    h = conv(f, conv_w, conv_b, nb)
-    h = layernorm(h, None, None, eps)
-    h = linear(h, w0, b0)
-    h = layernorm(h, None, None, eps, silu=True)
+    h = st(conv(f, conv_w, conv_b, nb))
+    h = st(layernorm(h, None, None, eps))
+    h = st(linear(h, w0, b0))
+    h = st(layernorm(h, None, None, eps, silu=True))
     skip = f if rows is None else f[rows]
-    return linear(h, w2, b2, skip)
+    return st(linear(h, w2, b2, skip))
 
 
 def attention(q, k, v, cu_q, cu_kv, scale=None, rows=None) -> np.ndarray:

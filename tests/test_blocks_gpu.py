@@ -8,6 +8,7 @@ import pytest
 import torch
 
 import oracle
+from tests import _tol
 
 pytestmark = pytest.mark.gpu
 
@@ -71,7 +72,21 @@ def test_convnext_block_matches_oracle(pkg, dev, dtype):
     assert out.coords is st.coords and out.feats.shape == (n, c)
     nbr = pkg.get_neighbor_map(st).nbr.cpu().numpy()
     rows = np.sort(rng.choice(n, 1500, replace=False))
-    ref = oracle.convnext_block(x64, nbr, cw64, cb64, w064, b064, w264, b264, 1e-6, rows=rows)
-    # intermediates are rounded to the storage type between the block's steps
-    tol = 1e-4 if dtype == torch.float32 else 5e-2
-    assert rel_err(out.feats.float().cpu().numpy()[rows], ref) <= tol
+    got = out.feats.float().cpu().numpy()[rows]
+    if dtype == torch.float32:
+        ref = oracle.convnext_block(x64, nbr, cw64, cb64, w064, b064, w264, b264, 1e-6, rows=rows)
+        assert rel_err(got, ref) <= 1e-4
+        return
+    # The block stores each step's tensor in bf16, as the TS block does: the oracle rounds its
+    # fp64 intermediates to bf16 at the same five points (round to nearest even), and the block
+    # must match it within the bf16 tolerance.  Against the unrounded fp64 block the five
+    # roundings add up to more (printed; bounded at 5e-2).
+    def to_bf16(a):
+        return torch.from_numpy(np.ascontiguousarray(a)).to(torch.bfloat16).double().numpy()
+    ref_r = oracle.convnext_block(x64, nbr, cw64, cb64, w064, b064, w264, b264, 1e-6, rows=rows,
+                                  store=to_bf16)
+    ref_u = oracle.convnext_block(x64, nbr, cw64, cb64, w064, b064, w264, b264, 1e-6, rows=rows)
+    e_r = _tol.check(got, ref_r, 2e-2, "convnext bf16 vs bf16-rounded oracle")
+    e_u = rel_err(got, ref_u)
+    print(f"  convnext bf16 vs unrounded fp64 oracle: norm-wise {e_u:.3e}", flush=True)
+    assert e_u <= 5e-2, e_u

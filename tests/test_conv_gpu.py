@@ -1,14 +1,15 @@
 """Sparse conv on the GPU vs the fp64 oracle.
 
 Tolerance (norm-wise relative, max|y - r| / max|r|, r computed in fp64 from the same rounded
-inputs and weights): fp32 <= 1e-4, fp16 / bf16 <= 2e-2.
+inputs and weights): fp32 <= 1e-4, fp16 / bf16 <= 2e-2.  The workload convs also assert the
+per-element allclose with atol = rtol * rms(r) (tests/_tol.py) and print both.
 """
 import numpy as np
 import pytest
 import torch
 
 import oracle
-from tests import _golden
+from tests import _golden, _tol
 
 pytestmark = pytest.mark.gpu
 
@@ -62,6 +63,9 @@ def _workload_conv(pkg, dev, workload, ci, co, dtype, sample_rows=None, seed=0, 
     if sample_rows is not None and sample_rows < n:
         rows = np.sort(np.random.default_rng(seed + 3).choice(n, sample_rows, replace=False))
     ref = oracle.conv(f64, w64, b64, nbr[rows])
+    # both halves of the tolerance definition: norm-wise (returned, asserted by the caller) and
+    # per-element allclose with atol = rtol * rms(r) (asserted here, printed beside it)
+    _tol.check(out[rows], ref, TOL[dtype], f"{workload} {ci}->{co} {dtype}")
     return rel_err(out[rows], ref), m, (f, w, b), out
 
 

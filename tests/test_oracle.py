@@ -284,3 +284,45 @@ def test_linear_vs_torch_functional():
     np.testing.assert_allclose(oracle.linear(x, w), x @ w.T, rtol=1e-12, atol=1e-12)
     # a transposed weight is caught
     assert not np.allclose(oracle.linear(x[:, :12], w[:, :12].T.copy()), x[:, :12] @ w[:, :12].T)
+
+
+def test_convnext_block_composition_and_store_rounding():
+    """oracle.convnext_block against the same five steps composed from torch.nn.functional (fp64;
+    the conv from oracle.conv, pinned above by the dense closed form), and its `store` rounding:
+    identity changes nothing, bf16 rounding leaves bf16-representable outputs within a few bf16
+    ulps of the unrounded block, and a planted step order (linear before the first LayerNorm) is
+    caught."""
+    rng = np.random.default_rng(19)
+    coords = np.unique(rng.integers(0, 6, (120, 3)), axis=0)
+    coords = np.concatenate([np.zeros((len(coords), 1), np.int64), coords], 1).astype(np.int32)
+    _, _, _, nbr = oracle.map_sorted(coords, 1, (6, 6, 6))
+    n, c, hid = len(coords), 8, 16
+    x = rng.standard_normal((n, c))
+    cw = rng.standard_normal((c, 3, 3, 3, c)) / np.sqrt(27 * c)
+    cb, w0, b0 = rng.standard_normal(c), rng.standard_normal((hid, c)), rng.standard_normal(hid)
+    w2, b2 = rng.standard_normal((c, hid)), rng.standard_normal(c)
+    T = torch.from_numpy
+    h = T(oracle.conv(x, cw, cb, nbr))
+    h = F.layer_norm(h, (c,), eps=1e-6)
+    h = F.linear(h, T(w0), T(b0))
+    h = F.silu(F.layer_norm(h, (hid,), eps=1e-6))
+    want = (T(x) + F.linear(h, T(w2), T(b2))).numpy()
+    got = oracle.convnext_block(x, nbr, cw, cb, w0, b0, w2, b2, 1e-6)
+    np.testing.assert_allclose(got, want, rtol=1e-10, atol=1e-10)
+    assert np.array_equal(oracle.convnext_block(x, nbr, cw, cb, w0, b0, w2, b2, 1e-6,
+                                                store=lambda a: a), got)
+
+    def to_bf16(a):
+        return torch.from_numpy(np.ascontiguousarray(a)).to(torch.bfloat16).double().numpy()
+    rounded = oracle.convnext_block(x, nbr, cw, cb, w0, b0, w2, b2, 1e-6, store=to_bf16)
+    assert np.array_equal(to_bf16(rounded), rounded)
+    err = np.abs(rounded - got).max() / np.abs(got).max()
+    assert 0 < err < 5e-2, err
+    rows = np.array([3, 7, 50])
+    assert np.array_equal(oracle.convnext_block(x, nbr, cw, cb, w0, b0, w2, b2, 1e-6, rows=rows,
+                                                store=to_bf16), rounded[rows])
+    # planted: the first linear before the first LayerNorm
+    hp = F.linear(T(oracle.conv(x, cw, cb, nbr)), T(w0), T(b0))
+    hp = F.silu(F.layer_norm(hp, (hid,), eps=1e-6))
+    planted = (T(x) + F.linear(hp, T(w2), T(b2))).numpy()
+    assert not np.allclose(planted, got, rtol=1e-3, atol=1e-3)
