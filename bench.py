@@ -93,69 +93,182 @@ ROCPROF_NAME = {"map_fill": "fill_columns_kernel<bitmap>", "map_mark": "mark_ker
                 "map_place": "place_kernel<int32>", "radix_fill": "fill_window_kernel<int32>",
                 "radix_buckets": "bucket_sort_kernel<int32>",
                 "radix_partition": "partition_kernel<int32>", "radix_pack": "pack_sort_kernel<int32>",
-                "radix_scan": "scan_kernel"}
+                "radix_scan": "scan_kernel", "attention": "attn_mma_kernel",
+                "layernorm": "layernorm_kernel", "layernorm_silu": "layernorm_kernel",
+                "conv_tile_cost": "tile_cost_kernel", "conv_tile_schedule": "tile_schedule_kernel"}
 
 
-def load_traffic(kernel: str):
-    """HBM bytes per launch of `kernel` measured by rocprofv3 FETCH_SIZE + WRITE_SIZE runs."""
-    p = ROOT / "profiles" / "traffic.json"
-    if not p.exists():
-        return None
+COUNTERS_FILE = ROOT / "profiles" / "workload_counters.json"
+
+
+def load_counters() -> dict:
+    """{workload: {kernel: record}} from profiles/workload_counters.json (profiling.py merge of
+    the per-workload rocprofv3 runs), or {}."""
+    if not COUNTERS_FILE.exists():
+        return {}
     try:
-        doc = json.loads(p.read_text())
+        return json.loads(COUNTERS_FILE.read_text()).get("workloads", {})
     except ValueError:
-        return None
-    rec = doc.get("kernels", {}).get(ROCPROF_NAME.get(kernel, kernel))
+        return {}
+
+
+def load_traffic(counters: dict, workload: str, kernel: str):
+    """HBM bytes per launch of `kernel` in `workload` (FETCH_SIZE + WRITE_SIZE runs)."""
+    rec = counters.get(workload, {}).get(ROCPROF_NAME.get(kernel, kernel))
     if not rec or rec.get("fetch_bytes") is None or rec.get("write_bytes") is None:
         return None
     return rec["fetch_bytes"] + rec["write_bytes"]
 
 
-def profile_pass(pkg, dev) -> None:
-    """Short fixed workload for rocprofv3 --pmc runs: a 256 MiB device copy (counter scale),
-    three map builds on map512, one conv of each conv workload, two subdivisions and one bf16
-    attention call."""
+def write_floor_record(ctx, nmap, n: int, fill_ms: float, steps: int) -> dict:
+    """The fill's store pattern alone (tsc_map_write_floor): the (N,27) rows written at the map's
+    original rows (perm, what the fill does) and at sequential rows, each launch timed with
+    hipEvents.  fill_over_floor = the fill's time / the scattered floor."""
+    import torch
+
+    out = torch.empty((n, 27), dtype=torch.int32, device=nmap.nbr.device)
+    res = {"kernel": "map_write_floor", "bytes_per_launch": 112 * n,
+           "note": "tsc_map_write_floor: 112 B per voxel (4 B row index in, 108 B row out), the "
+                   "fill's blocks, lanes and 12-byte stores without its loads and searches"}
+    for label, rows in (("scattered_ms", nmap.perm), ("sequential_ms", None)):
+        def run():
+            _check(ctx, ctx.lib.tsc_map_write_floor(ctx.bind(), None if rows is None else
+                                                    rows.data_ptr(), n, out.data_ptr()))
+        for _ in range(3):
+            run()
+        kt = kernel_times(ctx, run, steps)
+        res[label] = round(kt["map_write_floor"][0], 4)
+    res["scattered_gbps"] = round(112 * n / (res["scattered_ms"] / 1e3) / 1e9, 1)
+    res["fill_over_floor"] = round(fill_ms / res["scattered_ms"], 3)
+    log(f"write floor: scattered {res['scattered_ms']} ms ({res['scattered_gbps']} GB/s), "
+        f"sequential {res['sequential_ms']} ms; fill / floor = {res['fill_over_floor']}")
+    return res
+
+
+def _check(ctx, status: int) -> None:
+    if status:
+        raise RuntimeError(f"tsc status {status}: {ctx.lib.tsc_last_error().decode()}")
+
+
+# Workloads of the rocprofv3 counter runs (bench.py --profile-pass --workload NAME).  Each run
+# does a 256 MiB device copy (the counters' byte scale), sets the workload up, runs it
+# PROFILE_WARM times, synchronizes, then PROFILE_REPS more times; profiling.py keeps the last
+# PROFILE_REPS dispatches of every kernel, so each counter record belongs to one workload and to
+# warm launches.
+PROFILE_WARM, PROFILE_REPS = 3, 3
+PROFILE_WORKLOADS = ("map512", "conv64_f32", "narrow512_f16_32x32", "narrow512_f16_32x64",
+                     "wide128_bf16", "resblock64_bf16", "map_prep", "subdivide", "convnext",
+                     "attention_bf16")
+
+
+def profile_key(rec: dict) -> str:
+    """The PROFILE_WORKLOADS name a BENCH record's counters come from."""
+    if "profile_workload" in rec:
+        return rec["profile_workload"]
+    w = rec.get("workload", "")
+    if w == "narrow512_f16":
+        return f"narrow512_f16_{rec['ci']}x{rec['co']}"
+    return w
+
+
+def profile_setup(pkg, dev, name: str):
+    """(callable running the workload once, description) for one PROFILE_WORKLOADS entry."""
     import numpy as np
     import torch
 
     wl = pkg.workloads
+    dts = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16}
+    if name in ("map512", "map_prep"):
+        coords = wl.make_coords("map512")
+        cd = torch.from_numpy(coords).to(dev)
+        shape = wl.grid_shape("map512")
+        if name == "map512":
+            return (lambda: pkg.build_neighbor_map(cd, shape, 1, validate=False)), \
+                "tsc_map_build on map512"
+        nmap = pkg.build_neighbor_map(cd, shape, 1)
+
+        def prep():
+            pkg.map_conv_order(nmap.nbr, nmap.perm)
+            pkg.map_gather_plan(cd, nmap.nbr, 1, shape)
+        return prep, "tsc_map_conv_order + tsc_map_gather_plan on map512"
+    if name in ("subdivide", "convnext"):
+        coords = wl.make_coords("wide128_bf16")
+        n = coords.shape[0]
+        if name == "subdivide":
+            sc = torch.from_numpy(coords).to(dev)
+            sf = torch.from_numpy(wl.features(n, SUBDIV_C, 4)).to(dev).to(torch.bfloat16)
+            return (lambda: pkg.sparse_subdivide(sc, sf)), \
+                f"tsc_subdivide, wide128 voxels x {SUBDIV_C} bf16, all children"
+        c, hid, dt = CONVNEXT_C, CONVNEXT_HIDDEN, torch.bfloat16
+        g = torch.Generator(device="cpu").manual_seed(7)
+
+        def rnd(*shape, scale=1.0):
+            return (torch.randn(*shape, generator=g) * scale).to(dev).to(dt)
+        x = pkg.SparseTensor(rnd(n, c), torch.from_numpy(coords).to(dev))
+        blk = pkg.SparseConvNeXtBlock3d(torch.from_numpy(wl.conv_weight(c, c, 3)).to(dev).to(dt),
+                                       rnd(c, scale=0.1), rnd(hid, c, scale=c ** -0.5),
+                                       rnd(hid, scale=0.1), rnd(c, hid, scale=hid ** -0.5),
+                                       rnd(c, scale=0.1))
+        return (lambda: blk(x)), f"ConvNeXt block, wide128 voxels, C={c}, hidden={hid}, bf16"
+    if name == "attention_bf16":
+        ac = wl.make_coords("resblock64_bf16")
+        counts = np.bincount(ac[:, 0])
+        cu = torch.tensor([0, *np.cumsum(counts).tolist()], dtype=torch.int32, device=dev)
+        n = int(counts.sum())
+        q, k, v = (torch.randn((n, ATTN_HEADS, ATTN_DIM), device=dev).to(torch.bfloat16)
+                   for _ in range(3))
+        o = torch.empty_like(q)
+        return (lambda: pkg.sparse_attention(q, k, v, cu, out=o, max_seqlen_q=int(counts.max()))), \
+            f"varlen attention bf16, resblock64 voxels, {ATTN_HEADS} x {ATTN_DIM}"
+    base = name[:-6] if name.startswith("narrow512") else name
+    w = wl.WORKLOADS[base]
+    coords = wl.make_coords(base)
+    nmap = pkg.build_neighbor_map(torch.from_numpy(coords).to(dev), wl.grid_shape(base),
+                                  int(coords[:, 0].max()) + 1)
+    n = coords.shape[0]
+    ci, co = ((32, int(name[-2:])) if name.startswith("narrow512") else w.channels[0])
+    dt = dts[w.dtype]
+    f = torch.from_numpy(wl.features(n, ci, 1)).to(dev).to(dt)
+    if base == "resblock64_bf16":
+        ws = [(torch.from_numpy(wl.conv_weight(co, ci, 10 + i)).to(dev).to(dt),
+               torch.from_numpy(wl.conv_weight(co, ci, 20 + i)).to(dev).to(dt)) for i in range(4)]
+        zero = torch.zeros(co, device=dev, dtype=dt)
+        bufs = [torch.empty_like(f) for _ in range(2)]
+
+        def chain():
+            h = f
+            for i, (w1, w2) in enumerate(ws):
+                h = pkg.sparse_resblock(h, nmap, w1, zero, w2, zero, eps=1e-6, out=bufs[i % 2])
+        return chain, f"4 x ResBlock, resblock64 voxels, C={co}, bf16"
+    wt = torch.from_numpy(wl.conv_weight(co, ci, 2)).to(dev).to(dt)
+    b = torch.zeros(co, device=dev, dtype=dt)
+    o = torch.empty((n, co), device=dev, dtype=dt)
+    return (lambda: pkg.sparse_conv3d(f, wt, b, nmap, out=o)), \
+        f"conv {base} {ci}->{co} {w.dtype}"
+
+
+def profile_pass(pkg, dev, name: str) -> None:
+    """Short fixed run of one workload for rocprofv3: calibration copy, set-up, PROFILE_WARM
+    launches, then PROFILE_REPS launches (the ones profiling.py keeps)."""
+    import torch
+
+    if name not in PROFILE_WORKLOADS:
+        raise SystemExit(f"unknown profile workload {name!r}; one of {', '.join(PROFILE_WORKLOADS)}")
     c = torch.ones(1 << 26, dtype=torch.int32, device=dev)
     d = torch.empty_like(c)
     d.copy_(c)
     torch.cuda.synchronize()
     log("calibration copy 256 MiB done")
-    coords = wl.make_coords("map512")
-    cd = torch.from_numpy(coords).to(dev)
-    for _ in range(3):
-        pkg.build_neighbor_map(cd, wl.grid_shape("map512"), 1, validate=False)
+    run, desc = profile_setup(pkg, dev, name)
     torch.cuda.synchronize()
-    log("map builds done")
-    dts = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16}
-    for name in ("conv64_f32", "narrow512_f16", "wide128_bf16", "resblock64_bf16"):
-        w = wl.WORKLOADS[name]
-        co_np = coords if w.shell == "map512" else wl.make_coords(name)
-        nmap = pkg.build_neighbor_map(torch.from_numpy(co_np).to(dev), wl.grid_shape(name),
-                                      int(co_np[:, 0].max()) + 1)
-        n = co_np.shape[0]
-        for ci, co in w.channels:
-            f = torch.from_numpy(wl.features(n, ci, 1)).to(dev).to(dts[w.dtype])
-            wt = torch.from_numpy(wl.conv_weight(co, ci, 2)).to(dev).to(dts[w.dtype])
-            pkg.sparse_conv3d(f, wt, None, nmap)
-        torch.cuda.synchronize()
-        log(f"{name} conv done")
-    sc = torch.from_numpy(wl.make_coords("wide128_bf16")).to(dev)
-    sf = torch.randn((sc.shape[0], SUBDIV_C), device=dev).to(torch.bfloat16)
-    for _ in range(2):
-        pkg.sparse_subdivide(sc, sf)
+    log(f"{name}: {desc}: set up")
+    for _ in range(PROFILE_WARM):
+        run()
     torch.cuda.synchronize()
-    log("subdivide done")
-    ac = wl.make_coords("resblock64_bf16")
-    cu = torch.tensor([0, *np.cumsum(np.bincount(ac[:, 0])).tolist()], dtype=torch.int32, device=dev)
-    n = int(cu[-1])
-    q, k, v = (torch.randn((n, ATTN_HEADS, ATTN_DIM), device=dev).to(torch.bfloat16) for _ in range(3))
-    pkg.sparse_attention(q, k, v, cu)
+    for _ in range(PROFILE_REPS):
+        run()
     torch.cuda.synchronize()
-    log("attention done")
+    log(f"{name}: {PROFILE_WARM} warm-up + {PROFILE_REPS} profiled launches done")
 
 
 # Decoder upsample measured on the 2-voxel shell in 128^3 (4 x ~60k voxels) with 512 bf16
@@ -188,6 +301,7 @@ def subdivide_records(pkg, dev, steps, warmup) -> list:
         ms = time_steps(run, steps, warmup)
         nbytes = n * (16 + row) + m * (16 + row) + (0 if k is None else n)
         rec = {"workload": f"subdivide wide128 shell, {SUBDIV_C} bf16 channels, {label}",
+               "profile_workload": "subdivide" if k is None else None,
                "voxels": n, "children": m, "ms": round(ms, 4),
                "gbps_algorithmic": round(nbytes / (ms / 1e3) / 1e9, 1), "bound": "hbm",
                "roofline_frac": round(nbytes / (ms / 1e3) / PEAK_HBM, 4),
@@ -195,6 +309,10 @@ def subdivide_records(pkg, dev, steps, warmup) -> list:
                            for kn, (a, cnt) in kernel_times(ctx, run, 3).items()}}
         log(f"subdivide ({label}): {ms:.4f} ms, {rec['gbps_algorithmic']} GB/s, "
             f"roofline {rec['roofline_frac']}")
+        if rec["profile_workload"]:
+            attach_counters(rec, load_counters(), None, nbytes)
+        else:
+            del rec["profile_workload"]
         out.append(rec)
         del co, fo
         torch.cuda.empty_cache()
@@ -232,6 +350,7 @@ def convnext_record(pkg, dev, steps, warmup) -> dict:
     flops_lin = 2.0 * 2 * n * c * hid
     lin_ms = kt.get("linear", (0.0, 0))[0] * kt.get("linear", (0.0, 0))[1]
     rec = {"workload": f"ConvNeXt block on wide128 ({n} voxels), C={c}, hidden={hid}, bf16",
+           "profile_workload": "convnext",
            "voxels": n, "ms_per_block": round(ms, 4),
            "tflops_effective": round((flops_conv + flops_lin) / (ms / 1e3) / 1e12, 1),
            "linear_tflops": round(flops_lin / (lin_ms / 1e3) / 1e12, 1) if lin_ms else None,
@@ -239,6 +358,7 @@ def convnext_record(pkg, dev, steps, warmup) -> dict:
            "kernels": {k: {"avg_ms": round(a, 4), "launches_per_step": cnt} for k, (a, cnt) in kt.items()}}
     log(f"convnext block: {ms:.4f} ms, {rec['tflops_effective']} TFLOP/s eff, "
         f"linears {rec['linear_tflops']} TFLOP/s")
+    attach_counters(rec, load_counters())
     return rec
 
 
@@ -271,7 +391,7 @@ def attention_record(pkg, dev, steps) -> dict:
         o = torch.empty_like(q)
 
         def run():
-            return pkg.sparse_attention(q, k, v, cu_d, out=o)
+            return pkg.sparse_attention(q, k, v, cu_d, out=o, max_seqlen_q=int(counts.max()))
         reps = steps if dt == torch.bfloat16 else max(2, steps // 8)
         ms = time_steps(run, reps, 2)
         kt = kernel_times(ctx, run, 2)
@@ -280,6 +400,9 @@ def attention_record(pkg, dev, steps) -> dict:
                      "mfma_frac": round(tf / PEAK_MFMA[name], 4),
                      "kernels": {kk: {"avg_ms": round(a, 4), "launches_per_step": c}
                                  for kk, (a, c) in kt.items()}}
+        if dt == torch.bfloat16:
+            out[name]["profile_workload"] = "attention_bf16"
+            attach_counters(out[name], load_counters(), flops)
         log(f"attention {name}: {ms:.3f} ms, {tf / 1e12:.1f} TFLOP/s, "
             f"{tf / PEAK_MFMA[name]:.3f} of MFMA peak")
         del q, k, v, o
@@ -413,17 +536,6 @@ def conv_cpu_baseline(f_np, w_np, nbr, dtype: str, threads: int, budget_s: float
     return rec
 
 
-def load_counters():
-    """Per-kernel rocprofv3 counter averages (profiles/mfma_counters.json), or {}."""
-    p = ROOT / "profiles" / "mfma_counters.json"
-    if not p.exists():
-        return {}
-    try:
-        return json.loads(p.read_text()).get("kernels", {})
-    except ValueError:
-        return {}
-
-
 def cpu_baseline(coords_np, shape, threads: int) -> dict:
     import torch
 
@@ -464,21 +576,40 @@ def conv_record(name, ms, n, p, ci, co, dtype, extra=None) -> dict:
     return rec
 
 
-def attach_counters(rec: dict, counters: dict, flops: float | None = None) -> None:
-    """Add the rocprofv3 counter figures of the record's kernels (profiles/mfma_counters.json)."""
+def attach_counters(rec: dict, counters: dict, flops: float | None = None,
+                    alg_bytes: float | None = None) -> None:
+    """Add the rocprofv3 figures of the record's kernels, from the counter runs of the record's
+    own workload (profiles/workload_counters.json): MFMA busy, executed MFMA TFLOP/s, clock, HBM
+    bytes, the counter run's duration over this run's, and for the dominant kernel the executed
+    MFMA work over the valid-tap work and the HBM bytes over the algorithmic bytes."""
+    key = profile_key(rec)
+    wl = counters.get(key)
+    if not wl:
+        return
+    ks = rec.get("kernels", {})
+    dom = max(ks, key=lambda k: ks[k]["avg_ms"] * ks[k]["launches_per_step"]) if ks else None
     got = {}
-    for k in rec.get("kernels", {}):
-        c = counters.get(k)
+    for k, kr in ks.items():
+        c = wl.get(ROCPROF_NAME.get(k, k))
         if not c:
             continue
-        e = {key: round(c[key], 4) for key in ("mfma_busy", "mfma_tflops_hw", "avg_us") if key in c}
-        if flops and c.get("avg_us") and c.get("mfma_tflops_hw"):
-            # executed MFMA work over valid-tap work: > 1 means zero-padded taps were computed
+        e = {key2: round(c[key2], 4) for key2 in ("mfma_busy", "mfma_tflops_hw", "clock_ghz", "avg_us")
+             if key2 in c}
+        for b in ("fetch_bytes", "write_bytes"):
+            if b in c:
+                e[b] = c[b]
+        if kr.get("avg_ms"):
+            e["counter_run_over_bench_duration"] = round(c["avg_us"] / 1e3 / kr["avg_ms"], 3)
+        if k == dom and flops and c.get("mfma_tflops_hw"):
+            # > 1: zero-padded taps were multiplied too
             e["mfma_work_over_algorithmic"] = round(c["mfma_tflops_hw"] * 1e12 * c["avg_us"] * 1e-6
                                                     / flops, 3)
+        if k == dom and alg_bytes and "fetch_bytes" in c and "write_bytes" in c:
+            e["hbm_bytes_over_algorithmic"] = round((c["fetch_bytes"] + c["write_bytes"]) / alg_bytes, 3)
         got[k] = e
     if got:
-        rec["counters"] = {"source": "profiles/mfma_counters.txt", "kernels": got}
+        rec["counters"] = {"source": "profiles/workload_counters.txt", "workload": key,
+                           "kernels": got}
 
 
 def secondary(pkg, dev, steps, warmup, map512_coords, cpu_threads=None) -> list:
@@ -528,7 +659,9 @@ def secondary(pkg, dev, steps, warmup, map512_coords, cpu_threads=None) -> list:
                 rec = conv_record(name, ms, n, p, ci, co, w.dtype)
                 kt = kernel_times(pkg._lib.context(dev.index), conv, 3)
             rec["kernels"] = {k: {"avg_ms": round(a, 4), "launches_per_step": c} for k, (a, c) in kt.items()}
-            attach_counters(rec, counters, 2.0 * p * ci * co)
+            s_el = 4 if w.dtype == "float32" else 2
+            attach_counters(rec, counters, 2.0 * p * ci * co,
+                            n * ci * s_el + n * co * s_el + 27 * ci * co * s_el + co * s_el + 108 * n)
             if cpu_threads:
                 log(f"{name} {ci}->{co}: CPU conv_none baseline on {cpu_threads} threads ...")
                 rec["cpu_baseline"] = conv_cpu_baseline(wl.features(n, ci, 1),
@@ -553,7 +686,9 @@ def main() -> int:
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
     ap.add_argument("--profile-pass", action="store_true",
-                    help="run the short fixed workload used for rocprofv3 --pmc runs and exit")
+                    help="run one short fixed workload (--workload) for rocprofv3 runs and exit")
+    ap.add_argument("--workload", default="map512", choices=PROFILE_WORKLOADS,
+                    help="the --profile-pass workload")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -569,7 +704,7 @@ def main() -> int:
     pkg = __graft_entry__.load_package()
     dev = torch.device("cuda:0")
     if args.profile_pass:
-        profile_pass(pkg, dev)
+        profile_pass(pkg, dev, args.workload)
         return 0
     wl = pkg.workloads
     t0 = time.time()
@@ -592,7 +727,8 @@ def main() -> int:
     dom_ms = kt[dom][0]
     per_voxel = MAP_KERNEL_BYTES.get(dom)
     achieved = (per_voxel * n / (dom_ms / 1e3)) if per_voxel else None
-    traffic = load_traffic(dom)
+    counters = load_counters()
+    traffic = load_traffic(counters, "map512", dom)
     roofline = {"kernel": dom, "bound": "hbm",
                 "achieved": round(achieved / 1e9, 1) if achieved else None, "peak": PEAK_HBM / 1e9,
                 "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4) if achieved else None,
@@ -601,6 +737,9 @@ def main() -> int:
                 "kernels": {k: {"avg_ms": round(a, 4), "launches_per_step": c} for k, (a, c) in kt.items()}}
     log(f"dominant kernel {dom}: {dom_ms:.4f} ms; all: " +
         ", ".join(f"{k}={a:.4f}" for k, (a, c) in kt.items()))
+    roofline["write_floor"] = write_floor_record(ctx, nmap, n, dom_ms, args.steps)
+    roofline["profile_workload"] = "map512"
+    attach_counters(roofline, load_counters(), None, per_voxel * n if per_voxel else None)
     # One-time per coordinate set, cached with the map: the row order the convs use.
     order_ms = time_steps(lambda: pkg.map_conv_order(nmap.nbr, nmap.perm), args.steps, args.warmup)
     log(f"conv row order (tsc_map_conv_order): {order_ms:.4f} ms")

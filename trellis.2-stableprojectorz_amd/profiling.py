@@ -11,6 +11,15 @@
       per-kernel average FETCH_SIZE and WRITE_SIZE (KiB per dispatch) scaled to bytes by the
       same counters on a device copy of --calib-bytes bytes (the largest copy dispatch in the run)
 
+  python trellis.2-stableprojectorz_amd/profiling.py workload NAME TRACE.db MFMA.db FETCH.db \
+          WRITE.db OUT.json --last 3 --calib-bytes 268435456 --command "..."
+      one workload's record (a bench.py --profile-pass --workload NAME run under each of the four
+      rocprofv3 passes): per kernel, the averages over its last --last dispatches (the warm
+      launches) of duration, every counter, HBM bytes (FETCH_SIZE / WRITE_SIZE scaled by the
+      calibration copy) and the derived MFMA figures
+  python trellis.2-stableprojectorz_amd/profiling.py merge OUT.json OUT.txt IN.json...
+      the per-workload records in one file, {workload: {kernel: record}}, and a text summary
+
 Kernel names are shortened to the name the library's own profiler uses where possible
 (e.g. conv_mfma_kernel<__bf16,256,256,64,4,2,4,0> -> conv_mfma_kernel<bf16,256x256,k64,s4>).
 """
@@ -204,6 +213,93 @@ def counters(pmc_db: str, trace_db: str, out_json: str, out_txt: str, command: s
     open(out_txt, "w").write("\n".join(lines) + "\n")
 
 
+def _last_per_kernel(rows, last: int) -> dict:
+    """{short name: [values of its last `last` dispatches]} from (dispatch order, name, value)."""
+    per = defaultdict(list)
+    for _, name, val in sorted(rows, key=lambda r: r[0]):
+        per[name].append(val)
+    return {short_name(k): v[-last:] for k, v in per.items()
+            if "copyBuffer" not in k and "fillBuffer" not in k and "at::native" not in k}
+
+
+def _calib_scale(db: str, counter: str, calib_bytes: int) -> float:
+    rows = _rows(db, "select kernel_name, value, grid_size from counters_collection "
+                     f"where counter_name = '{counter}' and kernel_name like '%copyBuffer%'")
+    _, kib, _ = max(rows, key=lambda r: r[2])  # the largest copy is the calibration copy
+    return calib_bytes / (float(kib) * 1024.0)
+
+
+def workload(name: str, trace_db: str, mfma_db: str, fetch_db: str, write_db: str, out_json: str,
+             last: int, calib_bytes: int, command: str) -> None:
+    durs = _last_per_kernel(_rows(trace_db, "select dispatch_id, name, duration from kernels"), last)
+    counters = [r[0] for r in _rows(mfma_db, "select distinct counter_name from counters_collection")]
+    per_counter = {c: _last_per_kernel(_rows(mfma_db, "select dispatch_id, kernel_name, value from "
+                                                      f"counters_collection where counter_name = '{c}'"),
+                                       last) for c in counters}
+    fetch = _last_per_kernel(_rows(fetch_db, "select dispatch_id, kernel_name, value from "
+                                             "counters_collection where counter_name = 'FETCH_SIZE'"),
+                             last)
+    write = _last_per_kernel(_rows(write_db, "select dispatch_id, kernel_name, value from "
+                                             "counters_collection where counter_name = 'WRITE_SIZE'"),
+                             last)
+    fs = _calib_scale(fetch_db, "FETCH_SIZE", calib_bytes)
+    ws = _calib_scale(write_db, "WRITE_SIZE", calib_bytes)
+    res = {}
+    for k, d in durs.items():
+        rec = {"dispatches": len(d), "avg_us": sum(d) / len(d) / 1e3}
+        for c in counters:
+            v = per_counter[c].get(k)
+            if v:
+                rec[c] = sum(v) / len(v)
+        if k in fetch:
+            rec["fetch_bytes"] = round(sum(fetch[k]) / len(fetch[k]) * 1024 * fs)
+        if k in write:
+            rec["write_bytes"] = round(sum(write[k]) / len(write[k]) * 1024 * ws)
+        mops = sum(rec.get(c, 0.0) for c in rec if c.startswith("SQ_INSTS_VALU_MFMA_MOPS_"))
+        if mops:
+            rec["mfma_tflops_hw"] = mops * MOPS_FLOPS / (rec["avg_us"] * 1e-6) / 1e12
+        if rec.get("SQ_VALU_MFMA_BUSY_CYCLES") is not None and rec.get("GRBM_GUI_ACTIVE"):
+            xcd_cycles = rec["GRBM_GUI_ACTIVE"] / XCDS
+            rec["mfma_busy"] = rec["SQ_VALU_MFMA_BUSY_CYCLES"] / (xcd_cycles * SIMDS)
+            rec["clock_ghz"] = xcd_cycles / (rec["avg_us"] * 1e3)
+        res[k] = rec
+    doc = {"workload": name, "kernels": res, "command": command, "last_dispatches": last,
+           "calibration": {"copy_bytes": calib_bytes, "fetch_scale": fs, "write_scale": ws}}
+    open(out_json, "w").write(json.dumps(doc, indent=1) + "\n")
+
+
+def merge(out_json: str, out_txt: str, inputs: list) -> None:
+    docs = [json.loads(open(p).read()) for p in inputs]
+    merged = {"workloads": {d["workload"]: d["kernels"] for d in docs},
+              "commands": {d["workload"]: d["command"] for d in docs},
+              "calibration": {d["workload"]: d["calibration"] for d in docs},
+              "formulas": {"avg_us": "mean kernel-trace duration of the last dispatches",
+                           "fetch_bytes / write_bytes": "FETCH_SIZE / WRITE_SIZE (KiB) x 1024 x the "
+                                                        "scale a 256 MiB device copy gives",
+                           "mfma_tflops_hw": "sum(SQ_INSTS_VALU_MFMA_MOPS_*) * 512 / avg_us",
+                           "mfma_busy": "SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 * 1024 SIMDs)",
+                           "clock_ghz": "GRBM_GUI_ACTIVE / 8 / avg_us"}}
+    open(out_json, "w").write(json.dumps(merged, indent=1) + "\n")
+    lines = ["# rocprofv3 per-workload kernel records: the last dispatches of each kernel in a "
+             "bench.py --profile-pass --workload W run",
+             "# durations from --kernel-trace; counters from one --pmc run per counter set; HBM "
+             "bytes scaled by a 256 MiB device copy", ""]
+    for d in docs:
+        lines.append(f"## {d['workload']}")
+        lines.append(f"# commands: {d['command']}")
+        lines.append(f"{'kernel':52s} {'avg_us':>9s} {'fetch_MB':>9s} {'write_MB':>9s} "
+                     f"{'mfma_busy':>9s} {'hw_TF/s':>8s} {'GHz':>5s}")
+        for k, r in sorted(d["kernels"].items(), key=lambda kv: -kv[1]["avg_us"]):
+            def f(key, scale=1.0, fmt="{:9.2f}"):
+                v = r.get(key)
+                return fmt.format(v * scale) if v is not None else f"{'-':>9s}"
+            lines.append(f"{k:52s} {r['avg_us']:9.2f} {f('fetch_bytes', 1e-6)} "
+                         f"{f('write_bytes', 1e-6)} {f('mfma_busy', 1.0, '{:9.3f}')} "
+                         f"{f('mfma_tflops_hw', 1.0, '{:8.1f}')} {f('clock_ghz', 1.0, '{:5.2f}')}")
+        lines.append("")
+    open(out_txt, "w").write("\n".join(lines) + "\n")
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -224,7 +320,24 @@ def main() -> None:
     t.add_argument("out_txt")
     t.add_argument("--calib-bytes", type=int, default=256 << 20)
     t.add_argument("--command", default="")
+    w = sub.add_parser("workload")
+    for arg in ("name", "trace_db", "mfma_db", "fetch_db", "write_db", "out_json"):
+        w.add_argument(arg)
+    w.add_argument("--last", type=int, default=3)
+    w.add_argument("--calib-bytes", type=int, default=256 << 20)
+    w.add_argument("--command", default="")
+    m = sub.add_parser("merge")
+    m.add_argument("out_json")
+    m.add_argument("out_txt")
+    m.add_argument("inputs", nargs="+")
     a = ap.parse_args()
+    if a.cmd == "workload":
+        workload(a.name, a.trace_db, a.mfma_db, a.fetch_db, a.write_db, a.out_json, a.last,
+                 a.calib_bytes, a.command)
+        return
+    if a.cmd == "merge":
+        merge(a.out_json, a.out_txt, a.inputs)
+        return
     if a.cmd == "stats":
         stats(a.db, a.out, a.command)
     elif a.cmd == "counters":
