@@ -87,8 +87,8 @@ def kernel_times(ctx, fn, steps: int) -> dict:
     return {k: (ms / n, n / steps) for k, (ms, n) in res.items()}
 
 
-# Library profiler names -> the kernel names profiles/traffic.json uses (rocprofv3 symbols
-# shortened by trellis.2-stableprojectorz_amd/profiling.py).
+# Library profiler names -> the kernel names of profiles/workload_counters.json (rocprofv3
+# symbols shortened by trellis.2-stableprojectorz_amd/profiling.py).
 ROCPROF_NAME = {"map_fill": "fill_columns_kernel<bitmap>", "map_mark": "mark_kernel<int32>",
                 "map_place": "place_kernel<int32>", "radix_fill": "fill_window_kernel<int32>",
                 "radix_buckets": "bucket_sort_kernel<int32>",
