@@ -612,7 +612,44 @@ def attach_counters(rec: dict, counters: dict, flops: float | None = None,
                            "kernels": got}
 
 
-def secondary(pkg, dev, steps, warmup, map512_coords, cpu_threads=None) -> list:
+def copy_ceiling(dev, steps: int) -> dict:
+    """A 1 GiB device-to-device copy (torch): the HBM rate this box sustains for a plain
+    streaming kernel, counting the bytes read and the bytes written."""
+    import torch
+
+    a = torch.ones(1 << 28, dtype=torch.int32, device=dev)
+    b = torch.empty_like(a)
+    ms = time_steps(lambda: b.copy_(a), max(5, steps // 2), 3)
+    nbytes = 2 * a.numel() * 4
+    del a, b
+    torch.cuda.empty_cache()
+    rec = {"what": "torch copy of 1 GiB on the device (bytes read + written)", "ms": round(ms, 4),
+           "gbps": round(nbytes / (ms / 1e3) / 1e9, 1),
+           "hbm_frac": round(nbytes / (ms / 1e3) / PEAK_HBM, 4)}
+    log(f"copy ceiling: {rec['gbps']} GB/s ({rec['hbm_frac']} of HBM peak)")
+    return rec
+
+
+def dense_gemm_ceiling(dev, m: int, k: int, n: int, steps: int) -> dict:
+    """torch.matmul (hipBLASLt) in bf16 of a conv's implicit-GEMM shape with every tap present
+    (M = voxels, K = 27 * Ci, N = Co): the rate the chip's own GEMM library sustains on the
+    dense work of that shape, beside which the sparse conv's MFMA fraction is read."""
+    import torch
+
+    g = torch.Generator(device="cpu").manual_seed(3)
+    a = torch.randn((m, k), generator=g, dtype=torch.float32).to(torch.bfloat16).to(dev)
+    b = torch.randn((k, n), generator=g, dtype=torch.float32).to(torch.bfloat16).to(dev)
+    ms = time_steps(lambda: torch.matmul(a, b), max(3, steps // 4), 2)
+    flops = 2.0 * m * k * n
+    del a, b
+    torch.cuda.empty_cache()
+    return {"what": "torch.matmul bf16 (hipBLASLt), dense implicit-GEMM shape of the conv",
+            "shape_mkn": [m, k, n], "ms": round(ms, 4),
+            "tflops": round(flops / (ms / 1e3) / 1e12, 1),
+            "mfma_frac": round(flops / (ms / 1e3) / PEAK_MFMA["bfloat16"], 4)}
+
+
+def secondary(pkg, dev, steps, warmup, map512_coords, cpu_threads=None, copy=None) -> list:
     import numpy as np
     import torch
 
@@ -662,6 +699,14 @@ def secondary(pkg, dev, steps, warmup, map512_coords, cpu_threads=None) -> list:
             s_el = 4 if w.dtype == "float32" else 2
             attach_counters(rec, counters, 2.0 * p * ci * co,
                             n * ci * s_el + n * co * s_el + 27 * ci * co * s_el + co * s_el + 108 * n)
+            if rec["bound"] == "hbm" and copy:
+                rec["frac_of_copy_ceiling"] = round(rec["gbps_algorithmic"] / copy["gbps"], 4)
+            if rec["bound"] == "mfma" and w.dtype == "bfloat16":
+                rec["dense_gemm_ceiling"] = dense_gemm_ceiling(dev, n, 27 * ci, co, steps)
+                rec["frac_of_dense_gemm_ceiling"] = round(
+                    rec["tflops_effective"] / rec["dense_gemm_ceiling"]["tflops"], 4)
+                log(f"  dense GEMM ceiling {rec['dense_gemm_ceiling']['tflops']} TFLOP/s "
+                    f"({rec['dense_gemm_ceiling']['mfma_frac']} of peak)")
             if cpu_threads:
                 log(f"{name} {ci}->{co}: CPU conv_none baseline on {cpu_threads} threads ...")
                 rec["cpu_baseline"] = conv_cpu_baseline(wl.features(n, ci, 1),
@@ -738,6 +783,12 @@ def main() -> int:
     log(f"dominant kernel {dom}: {dom_ms:.4f} ms; all: " +
         ", ".join(f"{k}={a:.4f}" for k, (a, c) in kt.items()))
     roofline["write_floor"] = write_floor_record(ctx, nmap, n, dom_ms, args.steps)
+    copy = copy_ceiling(dev, args.steps)
+    roofline["copy_ceiling"] = copy
+    if achieved:
+        roofline["frac_of_copy_ceiling"] = round(achieved / 1e9 / copy["gbps"], 4)
+    roofline["build_frac_of_copy_ceiling"] = round(MAP_BYTES_PER_VOXEL * n / (ms / 1e3) / 1e9
+                                                   / copy["gbps"], 4)
     roofline["profile_workload"] = "map512"
     attach_counters(roofline, load_counters(), None, per_voxel * n if per_voxel else None)
     # One-time per coordinate set, cached with the map: the row order the convs use.
@@ -750,8 +801,10 @@ def main() -> int:
     sec = []
     if not args.no_secondary:
         sec = secondary(pkg, dev, args.steps, args.warmup, coords,
-                        None if args.no_cpu_baseline else args.cpu_threads)
-        sec += subdivide_records(pkg, dev, args.steps, args.warmup)
+                        None if args.no_cpu_baseline else args.cpu_threads, copy)
+        for r in subdivide_records(pkg, dev, args.steps, args.warmup):
+            r["frac_of_copy_ceiling"] = round(r["gbps_algorithmic"] / copy["gbps"], 4)
+            sec.append(r)
         sec.append(convnext_record(pkg, dev, args.steps, args.warmup))
         sec.append(attention_record(pkg, dev, args.steps))
         sec.append(safetensors_record(pkg, args.steps))

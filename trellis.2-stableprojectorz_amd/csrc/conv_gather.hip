@@ -218,7 +218,7 @@ __device__ __forceinline__ void mfma16<__bf16>(const uint4& a, const uint4& b, f
                                                 __builtin_bit_cast(bf16x8_t, b), acc, 0, 0, 0);
 }
 
-constexpr int kGWaves = 7;    // waves per block (one block per CU: LDS-bound)
+constexpr int kGWaves = 7;   // waves per block (one block per CU: LDS-bound)
 constexpr int kGStage = 208;  // LDS row slots per wave (slot 0 = zeros); tiles need d < 208
 constexpr int kGChunks = kGStage / 16;
 
@@ -246,6 +246,7 @@ __global__ void __launch_bounds__(64 * kGWaves)
   __shared__ uint4 sW[kTaps * 32 * 4];
   __shared__ uint4 sStage[kGWaves][kGStage * 4];
   __shared__ uint4 sTbl[kGWaves][kTableQ];
+  __shared__ int32_t sTaken;  // tiles of the block's range handed out so far
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int l16 = lane & 15, q = lane >> 4;
   const int j = lane >> 2, p = lane & 3;
@@ -255,6 +256,7 @@ __global__ void __launch_bounds__(64 * kGWaves)
   const int slot_in_half = halves == 2 ? (local >> 1) : local;
   const int blocks_in_half = (int)(gridDim.x >> 3) / halves;
   const int co0 = 32 * half;
+  if (tid == 0) sTaken = 0;
 
   // Weights (Co,27,32) of this column half: row co, piece p -> [(v*32 + co)*4 + (p ^ ((co>>1)&3))].
   const uint4* wq = (const uint4*)weight;
@@ -273,11 +275,30 @@ __global__ void __launch_bounds__(64 * kGWaves)
   uint4* const st = sStage[wid];
   uint4* const tb = sTbl[wid];
 
-  const int t_begin = xcd * tiles_per_xcd;
-  const int t_end = min(n_tiles, t_begin + tiles_per_xcd);
-  const int stride = blocks_in_half * kGWaves;
-  const int first = __builtin_amdgcn_readfirstlane(t_begin + slot_in_half * kGWaves + wid);
-  if (first >= t_end) return;
+  // Tiles are dealt at run time inside a block: the block owns a contiguous run of its XCD's tiles
+  // (adjacent Morton tiles, so its gathers share L2 lines) and each wave takes the next tile of the
+  // run from an LDS counter, so waves that drew short tiles take more and the block ends when its
+  // work does, not when the wave with the longest fixed share does.  The counter read for the
+  // tile after next is issued one tile ahead.  (A global counter per XCD measured 3x slower:
+  // atomics on one address serialize.)
+  const int xt_begin = xcd * tiles_per_xcd;
+  const int xt_count = max(0, min(n_tiles, xt_begin + tiles_per_xcd) - xt_begin);
+  const int per_block = (xt_count + blocks_in_half - 1) / blocks_in_half;
+  const int t_begin = xt_begin + min(xt_count, slot_in_half * per_block);
+  const int t_end = xt_begin + min(xt_count, (slot_in_half + 1) * per_block);
+  // The counter's address goes through a zero the compiler cannot see through: with a uniform
+  // address its atomic optimizer broadcasts the result at once (readfirstlane and a wait for
+  // every LDS operation in flight).
+  auto take_async = [&]() {  // counter value in lane 0, not yet waited for
+    int32_t z;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+    int32_t v = 0;
+    if (lane == 0) v = atomicAdd(&sTaken + z, 1);
+    return v;
+  };
+  auto tile_of = [&](int32_t pending) { return t_begin + __builtin_amdgcn_readfirstlane(pending); };
+  const int first = tile_of(take_async());
+  if (first < t_end) {
 
   // Prefetch of a tile is straight-line code: per-lane loads whose addresses are clamped (never
   // skipped), so the compiler can count them exactly.  Loads under per-chunk branches made it
@@ -335,7 +356,8 @@ __global__ void __launch_bounds__(64 * kGWaves)
   uint4 ta, tb2;
   load_tbl(cur, ta, tb2);
   int32_t row_n = prow[(int64_t)cur * kPlanRows + lane];
-  int next = __builtin_amdgcn_readfirstlane(cur + stride);
+  int next = tile_of(take_async());
+  int32_t pend = take_async();
   int nx = next < t_end ? next : cur;
   int32_t meta_n = load_meta(nx);
   load_idx(nx);
@@ -369,7 +391,8 @@ __global__ void __launch_bounds__(64 * kGWaves)
     gather(d);
     load_tbl(nx, ta, tb2);
     row_n = prow[(int64_t)nx * kPlanRows + lane];
-    const int nn = __builtin_amdgcn_readfirstlane(next + stride);
+    const int nn = tile_of(pend);
+    pend = take_async();
     const int nnx = nn < t_end ? nn : nx;
     meta_n = load_meta(nnx);
     load_idx(nnx);
@@ -483,6 +506,7 @@ __global__ void __launch_bounds__(64 * kGWaves)
     next = nn;
     nx = nnx;
   }
+  }  // first < t_end
 }
 
 template <typename T, int EPI>
