@@ -589,8 +589,12 @@ def attach_counters(rec: dict, counters: dict, flops: float | None = None,
     ks = rec.get("kernels", {})
     dom = max(ks, key=lambda k: ks[k]["avg_ms"] * ks[k]["launches_per_step"]) if ks else None
     got = {}
+    symbols = [ROCPROF_NAME.get(k, k) for k in ks]
     for k, kr in ks.items():
-        c = wl.get(ROCPROF_NAME.get(k, k))
+        sym = ROCPROF_NAME.get(k, k)
+        if symbols.count(sym) > 1:
+            continue  # one kernel symbol for several launches of the record: not separable
+        c = wl.get(sym)
         if not c:
             continue
         e = {key2: round(c[key2], 4) for key2 in ("mfma_busy", "mfma_tflops_hw", "clock_ghz", "avg_us")
