@@ -2,9 +2,12 @@
 
 The plan is checked against its definition on the CPU: rows are a permutation sorted by the
 Morton code of the coordinates, every (row, tap) slot names the neighbor the map gives, slots
-follow the stated order (own rows first, then first use in (tap, row) order), and the tap
-masks are the OR of presence.  The planned conv must equal the unplanned kernels bit for bit,
-including tiles that take its fallback path (more distinct rows than the LDS staging holds).
+follow the stated order (own rows first, then first use in (tap, row) order; a split tile —
+more distinct rows than the LDS staging holds, but each 32-row half fewer — orders them as rows
+only the first half uses, rows both use, rows only the second half uses, and stores the second
+half's slots minus the first group's size), and the tap masks are the OR of presence.  The
+planned conv must equal the unplanned kernels bit for bit, including split tiles and tiles that
+take its fallback path (more distinct rows than the staging holds even per half).
 """
 import numpy as np
 import pytest
@@ -15,7 +18,8 @@ import oracle
 pytestmark = pytest.mark.gpu
 
 TILE, SLOTS, TBL = 64, 256, 16 * 28 * 4
-STAGE = 208  # LDS row slots per wave in the planned kernel (tiles with more go the fallback path)
+STAGE = 208  # LDS row slots per wave in the planned kernel (tiles or halves with fewer are staged)
+SPLIT = 1 << 30  # count flag of a split tile: d | sA << 8 | aonly << 16 | SPLIT
 
 
 def _align(v):
@@ -70,7 +74,12 @@ def _check_plan(pkg, dev, coords, batch, shape, dil=(1, 1, 1)):
         if count[ti] < 0:
             assert len(distinct) > SLOTS - 1
             continue
-        assert count[ti] == len(distinct)
+        used_a, used_b = set(nb[:32][pres[:32]].tolist()), set(nb[32:][pres[32:]].tolist())
+        split = count[ti] >= SPLIT
+        d = int(count[ti]) & 0xff if split else int(count[ti])
+        assert d == len(distinct)
+        # split exactly when the tile exceeds the staging and each half fits it
+        assert split == (d >= STAGE and len(used_a) < STAGE and len(used_b) < STAGE)
         # expected slot order: own rows, then by first (tap, row) use
         seen, order = set(), []
         for i in range(TILE):
@@ -81,9 +90,17 @@ def _check_plan(pkg, dev, coords, batch, shape, dil=(1, 1, 1)):
                 e = nb[i, v]
                 if v != 13 and e >= 0 and e not in seen:
                     seen.add(e); order.append(e)
+        base = np.zeros(TILE, np.int64)
+        if split:
+            sa, aonly = (int(count[ti]) >> 8) & 0xff, (int(count[ti]) >> 16) & 0xff
+            assert sa == len(used_a) and aonly == len(used_a - used_b)
+            order = ([e for e in order if e in used_a and e not in used_b] +
+                     [e for e in order if e in used_a and e in used_b] +
+                     [e for e in order if e in used_b and e not in used_a])
+            base[32:] = aonly  # the second half's table stores slot - aonly
         assert np.array_equal(lst[ti, :len(order)], order)
-        s = slots[ti].transpose(2, 0, 1).reshape(TILE, 28)[:, :27]  # [row][tap]
-        got = np.where(s > 0, lst[ti][np.maximum(s.astype(np.int64) - 1, 0)], -1)
+        s = slots[ti].transpose(2, 0, 1).reshape(TILE, 28)[:, :27].astype(np.int64)  # [row][tap]
+        got = np.where(s > 0, lst[ti][np.maximum(s + base[:, None] - 1, 0)], -1)
         assert np.array_equal(got, nb)
     return m, count
 
@@ -108,7 +125,7 @@ def test_plan_dense_blocks_and_ragged_tail(pkg, dev):
     coords = coords[np.random.default_rng(2).permutation(len(coords))]
     print(f"  gather plan dense N={len(coords)}", flush=True)
     _, c1 = _check_plan(pkg, dev, coords, 1, (32, 32, 32))
-    assert c1.max() >= STAGE
+    assert (c1 >= SPLIT).any()
     _, c2 = _check_plan(pkg, dev, coords, 1, (32, 32, 32), (2, 2, 2))
     assert (c2 < 0).any()
 
@@ -152,9 +169,9 @@ def test_planned_equals_direct_map512(pkg, dev, dtype, co, epilogue):
 
 @pytest.mark.parametrize("dil", [(1, 1, 1), (2, 2, 2)])
 def test_planned_fallback_tiles_match(pkg, dev, dil):
-    """Dense block: tiles over the staging (dilation 1) and over the list (dilation 2) take the
-    neighbor-map path inside the planned kernel; results still equal the direct kernels and the
-    fp64 oracle."""
+    """Dense block: tiles over the staging run as two 32-row halves (dilation 1), tiles over the
+    list (dilation 2) take the neighbor-map path inside the planned kernel; results still equal
+    the direct kernels and the fp64 oracle."""
     g = np.stack(np.meshgrid(*[np.arange(12)] * 3, indexing="ij"), -1).reshape(-1, 3) + 4
     coords = np.concatenate([np.zeros((len(g), 1), np.int64), g], 1).astype(np.int32)
     coords = coords[np.random.default_rng(4).permutation(len(coords))]
@@ -219,3 +236,27 @@ def test_plan_64bit_morton_keys(pkg, dev):
     *_, planned, direct = _pair(pkg, dev, coords, 2, (2048, 2048, 2048), 32, 32, torch.float16,
                                 "bias")
     assert torch.equal(planned, direct)
+
+
+@pytest.mark.parametrize("co", [32, 64])
+def test_planned_two_voxel_shell_split_tiles(pkg, dev, co):
+    """A 2-voxel shell (what subdividing a 1-voxel shell gives): ~6 % of its Morton tiles exceed
+    the staging and run as split tiles, a few exceed it per half too.  Planned = direct, bit for
+    bit, and the plan marks both kinds."""
+    spec = pkg.workloads.ShellSpec(128, 50.0, 62.0, 2, 0.35, (10, 8))
+    coords = pkg.workloads.shell_coords(spec, 21, 1)
+    print(f"  planned conv 2-voxel shell N={len(coords)} 32->{co}", flush=True)
+    m, *_, planned, direct = _pair(pkg, dev, coords, 1, (128, 128, 128), 32, co, torch.float16,
+                                   "residual", seed=co)
+    assert torch.equal(planned, direct)
+    _, count, *_ = _decode(m.gather_plan(), len(coords))
+    assert (count >= SPLIT).sum() > 10
+
+
+def test_plan_two_voxel_shell_layout(pkg, dev):
+    """The plan of a small 2-voxel shell against its definition, split tiles included."""
+    spec = pkg.workloads.ShellSpec(64, 24.0, 30.0, 2, 0.35, (10, 8))
+    coords = pkg.workloads.shell_coords(spec, 22, 1)
+    print(f"  gather plan 2-voxel shell N={len(coords)}", flush=True)
+    _, count = _check_plan(pkg, dev, coords, 1, (64, 64, 64))
+    assert (count >= SPLIT).any()

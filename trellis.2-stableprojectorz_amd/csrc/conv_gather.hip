@@ -15,13 +15,21 @@
 // Plan buffer layout (all offsets 256-byte aligned, T = ceil(N/64) tiles):
 //   rows   int32 [T*64]        row of each tile position in Morton order, -1 past N
 //   count  int32 [T]           distinct neighbor rows of the tile (d <= 255), or -1 when the tile
-//                              has more (it is then computed from the neighbor map directly)
+//                              has more (it is then computed from the neighbor map directly);
+//                              a split tile (below) stores d | sA << 8 | aonly << 16 | 1 << 30
 //   rbm    uint32 [T*4]        taps present in any row of each 16-row block
 //   list   int32 [T*256]       distinct rows of the tile, in slot order (slot s = list[s-1])
 //   slots  uint8 [T][16][28][4] slot of (row 16*rb + i, tap v) at [i][v][rb]; 0 = absent
 // Slot order: the tile's own rows first (row r -> slot r+1), then by first use in (tap, row)
 // order, so the 16 rows of one (tap, row block) mostly sit in consecutive slots (distinct LDS
 // banks for the fragment reads).
+// Split tiles: a tile with more distinct rows than the conv's staging holds (d >= kPlanStage),
+// but whose two 32-row halves each need fewer (sA, sB < kPlanStage; a 4x4x4 block of a solid:
+// 216 rows, 144 per half), orders its rows as (rows only the first half uses, rows both use,
+// rows only the second half uses), each group in the order above.  The first half's rows are
+// then slots 1..sA and the second half's slots aonly+1..d (aonly = rows of the first group);
+// the second half's table entries are stored minus aonly, so each half stages its own rows
+// at 1.. and the conv computes the tile as two passes of 32 rows.
 
 #include <climits>
 #include <string>
@@ -59,6 +67,7 @@ constexpr int kTaps = 27;
 constexpr int kHash = 512;         // per-tile hash capacity (tiles past 255 rows overflow)
 constexpr int kHashShift = 23;     // 32 - log2(kHash)
 constexpr int kPrioWords = 56;     // 1792 priorities / 32
+constexpr int kOrderWords = 3 * kPrioWords;  // split tiles: (group, priority) sort keys
 constexpr int kPlanWaves = 4;
 constexpr int kTableQ = kPlanTableBytes / 16;  // 112 uint4 per tile table
 
@@ -72,8 +81,9 @@ __global__ void __launch_bounds__(64 * kPlanWaves)
                      int32_t* __restrict__ list_out, uint4* __restrict__ slots_out) {
   __shared__ __attribute__((aligned(16))) int32_t hkey[kPlanWaves][kHash];
   __shared__ __attribute__((aligned(16))) int32_t hval[kPlanWaves][kHash];  // min prio, then slot
-  __shared__ uint32_t pbits[kPlanWaves][kPrioWords];
-  __shared__ int32_t ppre[kPlanWaves][64];
+  __shared__ uint32_t pbits[kPlanWaves][kOrderWords];
+  __shared__ int32_t ppre[kPlanWaves][kOrderWords];
+  __shared__ uint32_t hgrp[kPlanWaves][kHash / 16];  // 2 bits per hash entry: halves using it
   __shared__ uint4 table[kPlanWaves][kTableQ];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int64_t t = (int64_t)blockIdx.x * kPlanWaves + w;
@@ -84,7 +94,8 @@ __global__ void __launch_bounds__(64 * kPlanWaves)
     ((int4*)hk)[i] = make_int4(-1, -1, -1, -1);
     ((int4*)hv)[i] = make_int4(INT_MAX, INT_MAX, INT_MAX, INT_MAX);
   }
-  if (lane < kPrioWords) pbits[w][lane] = 0u;
+  for (int i = lane; i < kOrderWords; i += 64) pbits[w][i] = 0u;
+  if (lane < kHash / 16) hgrp[w][lane] = 0u;
   for (int i = lane; i < kTableQ; i += 64) table[w][i] = make_uint4(0, 0, 0, 0);
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   __builtin_amdgcn_wave_barrier();
@@ -122,6 +133,7 @@ __global__ void __launch_bounds__(64 * kPlanWaves)
       }
       if (ok) {
         atomicMin(&hv[h], prio);
+        atomicOr(&hgrp[w][h >> 4], (lane < 32 ? 1u : 2u) << (2 * (h & 15)));
         hpos[v] = h;
       } else {
         full = true;
@@ -132,21 +144,27 @@ __global__ void __launch_bounds__(64 * kPlanWaves)
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-  // Distinct count and the set of their (distinct) minimum priorities.
-  int cnt = 0;
+  // Distinct count, and per half the rows it uses (split decision).
+  int cnt = 0, ca = 0, cb = 0;
   for (int i = lane; i < kHash / 4; i += 64) {
     const int4 k4 = ((const int4*)hk)[i];
-    const int4 v4 = ((const int4*)hv)[i];
-    const int kk[4] = {k4.x, k4.y, k4.z, k4.w}, vv[4] = {v4.x, v4.y, v4.z, v4.w};
+    const int kk[4] = {k4.x, k4.y, k4.z, k4.w};
 #pragma unroll
     for (int u = 0; u < 4; ++u)
       if (kk[u] >= 0) {
+        const int h = 4 * i + u;
+        const uint32_t g = (hgrp[w][h >> 4] >> (2 * (h & 15))) & 3u;
         ++cnt;
-        atomicOr(&pbits[w][vv[u] >> 5], 1u << (vv[u] & 31));
+        ca += g & 1u;
+        cb += g >> 1;
       }
   }
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off, 64);
+  for (int off = 32; off > 0; off >>= 1) {
+    cnt += __shfl_xor(cnt, off, 64);
+    ca += __shfl_xor(ca, off, 64);
+    cb += __shfl_xor(cb, off, 64);
+  }
   // Per-16-row tap masks.
   uint32_t m = present;
 #pragma unroll
@@ -156,23 +174,52 @@ __global__ void __launch_bounds__(64 * kPlanWaves)
     if (lane == 0) count_out[t] = -1;
     return;
   }
-  if (lane == 0) count_out[t] = cnt;
+  const bool split = cnt >= kPlanStage && ca < kPlanStage && cb < kPlanStage;
+  const int aonly = cnt - cb;  // rows only the first half uses
+  if (lane == 0)
+    count_out[t] = split ? (cnt | ca << 8 | aonly << 16 | 1 << 30) : cnt;
+  // Sort key of every distinct row: its minimum priority, for split tiles offset by its group.
+  for (int i = lane; i < kHash / 4; i += 64) {
+    const int4 k4 = ((const int4*)hk)[i];
+    const int4 v4 = ((const int4*)hv)[i];
+    const int kk[4] = {k4.x, k4.y, k4.z, k4.w}, vv[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (kk[u] >= 0) {
+        const int h = 4 * i + u;
+        const uint32_t g = (hgrp[w][h >> 4] >> (2 * (h & 15))) & 3u;
+        const int key = vv[u] + (split ? (g == 1u ? 0 : g == 3u ? 1 : 2) * kPrioWords * 32 : 0);
+        atomicOr(&pbits[w][key >> 5], 1u << (key & 31));
+      }
+  }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-  // Exclusive prefix of the priority-bit popcounts (56 words, one per lane).
-  const int pc = lane < kPrioWords ? __popc(pbits[w][lane]) : 0;
-  int incl = pc;
+  // Exclusive prefix of the key-bit popcounts (168 words, three consecutive ones per lane).
+  int pc[3], loc = 0;
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    pc[k] = lane < kPrioWords ? __popc(pbits[w][3 * lane + k]) : 0;
+    loc += pc[k];
+  }
+  int incl = loc;
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) {
     const int o = __shfl_up(incl, off, 64);
     if (lane >= off) incl += o;
   }
-  ppre[w][lane] = incl - pc;
+  if (lane < kPrioWords) {
+    int base = incl - loc;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      ppre[w][3 * lane + k] = base;
+      base += pc[k];
+    }
+  }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-  // Slot = 1 + rank of the row's minimum priority.
+  // Slot = 1 + rank of the row's sort key.
   int32_t* const list = list_out + t * kPlanSlots;
   for (int i = lane; i < kHash / 4; i += 64) {
     const int4 k4 = ((const int4*)hk)[i];
@@ -182,7 +229,9 @@ __global__ void __launch_bounds__(64 * kPlanWaves)
 #pragma unroll
     for (int u = 0; u < 4; ++u)
       if (kk[u] >= 0) {
-        const int p = vv[u];
+        const int h = 4 * i + u;
+        const uint32_t g = (hgrp[w][h >> 4] >> (2 * (h & 15))) & 3u;
+        const int p = vv[u] + (split ? (g == 1u ? 0 : g == 3u ? 1 : 2) * kPrioWords * 32 : 0);
         const int rank = ppre[w][p >> 5] + __popc(pbits[w][p >> 5] & ((1u << (p & 31)) - 1u));
         list[rank] = kk[u];
         vv[u] = rank + 1;
@@ -194,9 +243,10 @@ __global__ void __launch_bounds__(64 * kPlanWaves)
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
   uint8_t* const tb = (uint8_t*)table[w];
   const int i16 = lane & 15, rb = lane >> 4;
+  const int slot_base = split && lane >= 32 ? aonly : 0;  // second half of a split tile
 #pragma unroll
   for (int v = 0; v < kTaps; ++v)
-    if (hpos[v] >= 0) tb[(i16 * 28 + v) * 4 + rb] = (uint8_t)hv[hpos[v]];
+    if (hpos[v] >= 0) tb[(i16 * 28 + v) * 4 + rb] = (uint8_t)(hv[hpos[v]] - slot_base);
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
@@ -219,7 +269,7 @@ __device__ __forceinline__ void mfma16<__bf16>(const uint4& a, const uint4& b, f
 }
 
 constexpr int kGWaves = 7;   // waves per block (one block per CU: LDS-bound)
-constexpr int kGStage = 208;  // LDS row slots per wave (slot 0 = zeros); tiles need d < 208
+constexpr int kGStage = kPlanStage;  // LDS row slots per wave (slot 0 = zeros)
 constexpr int kGChunks = kGStage / 16;
 
 // Wave-level tile loop, one block per CU, blocks split between column halves for Co = 64
@@ -232,8 +282,13 @@ constexpr int kGChunks = kGStage / 16;
 //           two-deep pipeline (fragments of tap k+1 in flight during the MFMAs of tap k)
 //   overlap while tile t computes, tile t+1's rows and slot table are in flight and tile t+2's
 //           list indices are loaded
-// Tiles whose distinct rows exceed the staging (count -1 or >= kGStage) read their B fragments
-// from global memory through the neighbor map instead.
+// Split tiles (the plan's count says which) run as two units of the same pipeline, one per
+// 32-row half: the first stages slots 1..sA, the second the list from entry aonly on, with the
+// other half's table bytes masked to slot 0 (its rows add zero products, as absent taps do) and
+// the taps of the half's row blocks.  Each row still sums its taps in tap order, so the result
+// is the same bits as a one-pass tile.  Tiles whose distinct rows exceed the staging otherwise
+// (count -1, or >= kGStage without a split) read their B fragments from global memory through
+// the neighbor map instead.
 template <typename T, int EPI>
 __global__ void __launch_bounds__(64 * kGWaves)
     conv_gather_kernel(const T* __restrict__ feats, const T* __restrict__ weight,
@@ -305,14 +360,37 @@ __global__ void __launch_bounds__(64 * kGWaves)
   // wait for every outstanding load before each dependent one (one vmcnt counts all loads in
   // order), which serialised a tile's ~20 index and row loads into one round trip each.
   //   meta  one load: lanes 0-3 the tile's four 16-row tap masks, lane 4 its distinct-row count
-  //   idx   the list entries of slots 16c + j (always inside the tile's kPlanSlots entries)
+  //   idx   the list entries of slots off + 16c + j (clamped to the tile's kPlanSlots entries)
   //   rows  row idx[c] piece p for slots below the count, else row 0 (valid, never staged)
   auto load_meta = [&](int t) {
     return lane < 4 ? (int32_t)prbm[t * 4 + lane] : pcount[t];
   };
-  auto meta_count = [&](int32_t meta) {
+  // A unit of work: a whole tile, or one half of a split tile (second = the second half).
+  struct Unit {
+    int g;           // rows to stage (-1: the tile reads through the neighbor map)
+    uint32_t pmask;  // table bytes (row blocks) of this unit
+    uint32_t taps;   // taps any of its row blocks uses
+    bool first;      // first half of a split tile: the second half follows, no epilogue yet
+    bool second;     // second half: accumulators carried over from the first
+  };
+  auto decode = [&](int32_t meta, bool second) {
     const int dd = __builtin_amdgcn_readlane(meta, 4);
-    return dd < kGStage ? dd : -1;  // -1: not staged
+    uint32_t mk[4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) mk[rb] = (uint32_t)__builtin_amdgcn_readlane(meta, rb);
+    Unit u{dd >= 0 && dd < kGStage ? dd : -1, 0xffffffffu, mk[0] | mk[1] | mk[2] | mk[3], false,
+           false};
+    if (dd >= 0 && (dd & (1 << 30))) {
+      if (!second) {
+        u = Unit{(dd >> 8) & 0xff, 0x0000ffffu, mk[0] | mk[1], true, false};
+      } else {
+        u = Unit{(dd & 0xff) - ((dd >> 16) & 0xff), 0xffff0000u, mk[2] | mk[3], false, true};
+      }
+    }
+    return u;
+  };
+  auto second_offset = [&](int32_t meta) {  // list entry of the second half's first slot
+    return (__builtin_amdgcn_readlane(meta, 4) >> 16) & 0xff;
   };
   typedef uint32_t xvec_t __attribute__((ext_vector_type(4 * kGChunks)));
   int32_t idx[kGChunks];
@@ -320,10 +398,10 @@ __global__ void __launch_bounds__(64 * kGWaves)
   auto chunk_mask = [](int d) {
     return d > 0 ? __builtin_amdgcn_readfirstlane((1u << ((d + 15) >> 4)) - 1u) : 0u;
   };
-  auto load_idx = [&](int t) {
+  auto load_idx = [&](int t, int off) {
     const int32_t* list = plist + (int64_t)t * kPlanSlots;
 #pragma unroll
-    for (int c = 0; c < kGChunks; ++c) idx[c] = list[16 * c + j];
+    for (int c = 0; c < kGChunks; ++c) idx[c] = list[min(off + 16 * c + j, kPlanSlots - 1)];
   };
   auto gather = [&](int d) {
 #pragma unroll
@@ -343,29 +421,36 @@ __global__ void __launch_bounds__(64 * kGWaves)
     tb2 = tq[64 + (lane < kTableQ - 64 ? lane : 0)];
   };
 
-  // Prologue: the first tile's rows gathered and its table loaded; the next tile's metadata and
+  // Prologue: the first unit's rows gathered and its table loaded; the next unit's metadata and
   // indices.  A missing next tile repeats the current one (its loads stay in bounds, unused).
+  // `pend` always holds the counter take for the next new tile; the second half of a split tile
+  // follows its first half without one.
   int cur = first;
   int32_t meta = load_meta(cur);
-  load_idx(cur);
-  int d = meta_count(meta);
-  uint32_t m[4];
-#pragma unroll
-  for (int rb = 0; rb < 4; ++rb) m[rb] = (uint32_t)__builtin_amdgcn_readlane(meta, rb);
-  gather(d);
+  load_idx(cur, 0);
+  Unit uc = decode(meta, false);
+  gather(uc.g);
   uint4 ta, tb2;
   load_tbl(cur, ta, tb2);
   int32_t row_n = prow[(int64_t)cur * kPlanRows + lane];
-  int next = tile_of(take_async());
   int32_t pend = take_async();
+  int next;
+  bool next_second = uc.first;
+  if (next_second) {
+    next = cur;
+  } else {
+    next = tile_of(pend);
+    pend = take_async();
+  }
   int nx = next < t_end ? next : cur;
   int32_t meta_n = load_meta(nx);
-  load_idx(nx);
+  load_idx(nx, next_second ? second_offset(meta) : 0);
+  f32x4_t acc[4][2];
 
   for (;;) {
     // Stage tile `cur`: rows and slot table into the wave's LDS.
     __builtin_amdgcn_wave_barrier();
-    const uint32_t cm = chunk_mask(d);
+    const uint32_t cm = chunk_mask(uc.g);
 #pragma unroll
     for (int c = 0; c < kGChunks; ++c)
       if ((cm >> c) & 1u) {
@@ -374,34 +459,42 @@ __global__ void __launch_bounds__(64 * kGWaves)
           st[s * 4 + (p ^ ((s >> 1) & 3))] = make_uint4(x[4 * c], x[4 * c + 1], x[4 * c + 2],
                                                         x[4 * c + 3]);
       }
-    tb[lane] = ta;
-    if (lane < kTableQ - 64) tb[64 + lane] = tb2;
+    // The unit's row blocks only: the other half of a split tile reads slot 0.
+    const uint32_t pm = uc.pmask;
+    tb[lane] = make_uint4(ta.x & pm, ta.y & pm, ta.z & pm, ta.w & pm);
+    if (lane < kTableQ - 64) tb[64 + lane] = make_uint4(tb2.x & pm, tb2.y & pm, tb2.z & pm, tb2.w & pm);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const uint32_t mc[4] = {m[0], m[1], m[2], m[3]};
-    const bool staged = d >= 0;
+    const Unit u = uc;
+    const bool staged = u.g >= 0;
     int32_t row_c = row_n < N ? row_n : -1;
-    // Tile `next` (or `cur` again at the end): rows, table and row list go out now; the tile
+    // Unit `next` (or `cur` again at the end): rows, table and row list go out now; the unit
     // after it gets its metadata and indices.
     const bool has_next = next < t_end;
-    d = meta_count(meta_n);
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb) m[rb] = (uint32_t)__builtin_amdgcn_readlane(meta_n, rb);
-    gather(d);
+    uc = decode(meta_n, next_second);
+    gather(uc.g);
     load_tbl(nx, ta, tb2);
     row_n = prow[(int64_t)nx * kPlanRows + lane];
-    const int nn = tile_of(pend);
-    pend = take_async();
+    int nn;
+    const bool nn_second = uc.first;
+    if (nn_second) {
+      nn = next;
+    } else {
+      nn = tile_of(pend);
+      pend = take_async();
+    }
     const int nnx = nn < t_end ? nn : nx;
+    const int nn_off = nn_second ? second_offset(meta_n) : 0;
     meta_n = load_meta(nnx);
-    load_idx(nnx);
-    f32x4_t acc[4][2];
+    load_idx(nnx, nn_off);
+    if (!u.second) {
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb)
+      for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-      for (int cb = 0; cb < 2; ++cb) acc[rb][cb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    const uint32_t tm = mc[0] | mc[1] | mc[2] | mc[3];
+        for (int cb = 0; cb < 2; ++cb) acc[rb][cb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+    const uint32_t tm = u.taps;
     auto rd_a = [&](int v, uint4 (&a)[2]) {
 #pragma unroll
       for (int cb = 0; cb < 2; ++cb) {
@@ -463,12 +556,14 @@ __global__ void __launch_bounds__(64 * kGWaves)
       }
     }
 
-    // Epilogue: lane (l16, q) owns row 16*rb + l16, columns co0 + 16*cb + 4q .. +3.  Residual
-    // values are all loaded before the first store (rows past N read row 0, not stored); each
-    // element is read and written by the same lane, so the output may alias the residual.
+    // Epilogue (after the second half of a split tile): lane (l16, q) owns row 16*rb + l16,
+    // columns co0 + 16*cb + 4q .. +3.  Residual values are all loaded before the first store
+    // (rows past N read row 0, not stored); each element is read and written by the same lane, so
+    // the output may alias the residual.
     struct alignas(4 * sizeof(T)) V4 {
       T v[4];
     };
+    if (!u.first) {
     int32_t rows[4];
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) rows[rb] = __shfl(row_c, rb * 16 + l16, 64);
@@ -501,9 +596,11 @@ __global__ void __launch_bounds__(64 * kGWaves)
         *(V4*)(out + (int64_t)row * co_total + c) = y;
       }
     }
+    }  // !u.first
     if (!has_next) break;
     cur = next;
     next = nn;
+    next_second = nn_second;
     nx = nnx;
   }
   }  // first < t_end

@@ -185,6 +185,9 @@ bool conv_fuses_ln(const ConvArgs& a);
 // ---- gather plan + planned narrow conv (conv_gather.hip) ----
 constexpr int kPlanRows = 64;                   // rows per plan tile
 constexpr int kPlanSlots = 256;                 // distinct-row list capacity per tile
+constexpr int kPlanStage = 208;                 // LDS row slots per wave of the planned conv
+                                                // (slot 0 = zeros): staged tiles and halves
+                                                // have fewer distinct rows
 constexpr int kPlanTableBytes = 16 * 28 * 4;    // slot table per tile: [16][28 taps][4 blocks]
 struct PlanLayout {
   int64_t T;                                    // tiles
