@@ -10,6 +10,8 @@ set, inputs already resident in HBM.  value = algorithmic bytes (128 B/voxel: 16
 TFLOP/s counting only valid taps, algorithmic GB/s, roofline fraction):
   conv64_f32       conv 64->64 fp32, ~25k voxels (64^3, 2-voxel shell)
   narrow512_f16    conv 32->32 and 32->64 fp16 on the map512 voxels
+  narrow512s2_f16  the same convs on ~3.0M voxels of a 2-voxel shell in 512^3 (the thickness a
+                   subdivided 1-voxel shell has), beside the unplanned kernel's time
   wide128_bf16     conv 512->512 bf16, 4 x ~61k voxels (128^3 shells)
   resblock64_bf16  4 x ResBlock (conv-LN-SiLU-conv-+x) at C=1024 bf16, 2 x ~32k voxels
 and the decoder upsample (tsc_subdivide) on the wide128 voxels with 512 bf16 channels, all 8
@@ -151,13 +153,12 @@ def _check(ctx, status: int) -> None:
 
 
 # Workloads of the rocprofv3 counter runs (bench.py --profile-pass --workload NAME).  Each run
-# does a 256 MiB device copy (the counters' byte scale), sets the workload up, runs it
-# PROFILE_WARM times, synchronizes, then PROFILE_REPS more times; profiling.py keeps the last
-# PROFILE_REPS dispatches of every kernel, so each counter record belongs to one workload and to
-# warm launches.
+# sets the workload up, runs it PROFILE_WARM times, makes a 256 MiB device copy (the counters'
+# byte scale), then runs it PROFILE_REPS more times; profiling.py keeps the dispatches after the
+# copy, so each counter record belongs to one workload and to warm launches.
 PROFILE_WARM, PROFILE_REPS = 3, 3
 PROFILE_WORKLOADS = ("map512", "conv64_f32", "narrow512_f16_32x32", "narrow512_f16_32x64",
-                     "wide128_bf16", "resblock64_bf16", "map_prep", "subdivide", "convnext",
+                     "narrow512s2_f16_32x32", "narrow512s2_f16_32x64", "wide128_bf16", "resblock64_bf16", "map_prep", "subdivide", "convnext",
                      "attention_bf16")
 
 
@@ -166,8 +167,8 @@ def profile_key(rec: dict) -> str:
     if "profile_workload" in rec:
         return rec["profile_workload"]
     w = rec.get("workload", "")
-    if w == "narrow512_f16":
-        return f"narrow512_f16_{rec['ci']}x{rec['co']}"
+    if w in ("narrow512_f16", "narrow512s2_f16"):
+        return f"{w}_{rec['ci']}x{rec['co']}"
     return w
 
 
@@ -248,23 +249,25 @@ def profile_setup(pkg, dev, name: str):
 
 
 def profile_pass(pkg, dev, name: str) -> None:
-    """Short fixed run of one workload for rocprofv3: calibration copy, set-up, PROFILE_WARM
-    launches, then PROFILE_REPS launches (the ones profiling.py keeps)."""
+    """Short fixed run of one workload for rocprofv3: set-up, PROFILE_WARM launches, the
+    calibration copy (256 MiB device copy: the counters' byte scale, and the mark after which
+    profiling.py counts dispatches), then PROFILE_REPS launches (the ones profiling.py keeps)."""
     import torch
 
     if name not in PROFILE_WORKLOADS:
         raise SystemExit(f"unknown profile workload {name!r}; one of {', '.join(PROFILE_WORKLOADS)}")
-    c = torch.ones(1 << 26, dtype=torch.int32, device=dev)
-    d = torch.empty_like(c)
-    d.copy_(c)
-    torch.cuda.synchronize()
-    log("calibration copy 256 MiB done")
     run, desc = profile_setup(pkg, dev, name)
     torch.cuda.synchronize()
     log(f"{name}: {desc}: set up")
     for _ in range(PROFILE_WARM):
         run()
     torch.cuda.synchronize()
+    c = torch.ones(1 << 26, dtype=torch.int32, device=dev)
+    d = torch.empty_like(c)
+    d.copy_(c)
+    torch.cuda.synchronize()
+    del c, d
+    log("calibration copy 256 MiB done")
     for _ in range(PROFILE_REPS):
         run()
     torch.cuda.synchronize()
@@ -661,7 +664,8 @@ def secondary(pkg, dev, steps, warmup, map512_coords, cpu_threads=None, copy=Non
     counters = load_counters()
     out = []
     dts = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16}
-    for name in ("conv64_f32", "narrow512_f16", "wide128_bf16", "resblock64_bf16"):
+    for name in ("conv64_f32", "narrow512_f16", "narrow512s2_f16", "wide128_bf16",
+                 "resblock64_bf16"):
         w = wl.WORKLOADS[name]
         coords = map512_coords if w.shell == "map512" else wl.make_coords(name)
         shape = wl.grid_shape(name)
@@ -699,6 +703,11 @@ def secondary(pkg, dev, steps, warmup, map512_coords, cpu_threads=None, copy=Non
                 ms = time_steps(conv, steps, warmup)
                 rec = conv_record(name, ms, n, p, ci, co, w.dtype)
                 kt = kernel_times(pkg._lib.context(dev.index), conv, 3)
+                if name.startswith("narrow512"):
+                    # the same conv through the neighbor table alone (no gather plan)
+                    rec["unplanned_ms"] = round(time_steps(
+                        lambda: pkg.sparse_conv3d(f, wt, b, nmap.nbr, out=o), steps, warmup), 4)
+                    log(f"  unplanned kernel: {rec['unplanned_ms']} ms")
             rec["kernels"] = {k: {"avg_ms": round(a, 4), "launches_per_step": c} for k, (a, c) in kt.items()}
             s_el = 4 if w.dtype == "float32" else 2
             attach_counters(rec, counters, 2.0 * p * ci * co,

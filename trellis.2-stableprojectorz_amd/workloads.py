@@ -34,6 +34,7 @@ class ShellSpec:
 SHELLS = {
     "conv64": ShellSpec(64, 20.0, 30.0, 2, 0.30, (6, 5)),
     "map512": ShellSpec(512, 200.0, 250.0, 1, 0.35, (10, 8)),
+    "map512s2": ShellSpec(512, 200.0, 250.0, 2, 0.35, (10, 8)),
     "wide128": ShellSpec(128, 34.0, 45.0, 2, 0.30, (7, 6)),
     "res64": ShellSpec(64, 22.0, 27.0, 2, 0.40, (8, 7)),
 }
@@ -120,6 +121,9 @@ WORKLOADS = {
                        "neighbor-map build, ~1.5M voxels, 1-voxel shell in 512^3, shuffled"),
     "narrow512_f16": Workload("narrow512_f16", "map512", 1, 202, ((32, 32), (32, 64)), "float16",
                               "conv3x3x3 32->32 and 32->64 fp16, ~1.5M voxels in 512^3"),
+    "narrow512s2_f16": Workload("narrow512s2_f16", "map512s2", 1, 202, ((32, 32), (32, 64)),
+                                "float16", "conv3x3x3 32->32 and 32->64 fp16, ~3.0M voxels of a "
+                                "2-voxel shell in 512^3 (the thickness subdivision gives)"),
     "wide128_bf16": Workload("wide128_bf16", "wide128", 4, 404, ((512, 512),), "bfloat16",
                              "conv3x3x3 512->512 bf16, 4 x ~60k voxels, 2-voxel shells in 128^3"),
     "resblock64_bf16": Workload("resblock64_bf16", "res64", 2, 505, ((1024, 1024),), "bfloat16",
