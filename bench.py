@@ -11,7 +11,8 @@ TFLOP/s counting only valid taps, algorithmic GB/s, roofline fraction):
   conv64_f32       conv 64->64 fp32, ~25k voxels (64^3, 2-voxel shell)
   narrow512_f16    conv 32->32 and 32->64 fp16 on the map512 voxels
   narrow512s2_f16  the same convs on ~3.0M voxels of a 2-voxel shell in 512^3 (the thickness a
-                   subdivided 1-voxel shell has), beside the unplanned kernel's time
+                   subdivided 1-voxel shell has); both narrow workloads also time the unplanned
+                   (direct) kernel in the map's row order
   wide128_bf16     conv 512->512 bf16, 4 x ~61k voxels (128^3 shells)
   resblock64_bf16  4 x ResBlock (conv-LN-SiLU-conv-+x) at C=1024 bf16, 2 x ~32k voxels
 and the decoder upsample (tsc_subdivide) on the wide128 voxels with 512 bf16 channels, all 8
@@ -704,10 +705,13 @@ def secondary(pkg, dev, steps, warmup, map512_coords, cpu_threads=None, copy=Non
                 rec = conv_record(name, ms, n, p, ci, co, w.dtype)
                 kt = kernel_times(pkg._lib.context(dev.index), conv, 3)
                 if name.startswith("narrow512"):
-                    # the same conv through the neighbor table alone (no gather plan)
+                    # the same conv without the gather plan: the direct kernel in the map's
+                    # cached row order (what an order argument selects)
+                    order = nmap.conv_order()
                     rec["unplanned_ms"] = round(time_steps(
-                        lambda: pkg.sparse_conv3d(f, wt, b, nmap.nbr, out=o), steps, warmup), 4)
-                    log(f"  unplanned kernel: {rec['unplanned_ms']} ms")
+                        lambda: pkg.sparse_conv3d(f, wt, b, nmap, order=order, out=o), steps,
+                        warmup), 4)
+                    log(f"  unplanned kernel (row order): {rec['unplanned_ms']} ms")
             rec["kernels"] = {k: {"avg_ms": round(a, 4), "launches_per_step": c} for k, (a, c) in kt.items()}
             s_el = 4 if w.dtype == "float32" else 2
             attach_counters(rec, counters, 2.0 * p * ci * co,
