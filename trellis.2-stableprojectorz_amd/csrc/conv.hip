@@ -201,6 +201,37 @@ inline int32_t tile_grid_per_xcd(int32_t m_tiles, int32_t n_tiles) {
 
 constexpr int kTaps = 27;
 
+// The tile's (row, tap) neighbor indices into LDS (sNbr[r*27 + v], -1 = absent) and the OR of
+// the taps present, over this thread's entries j = tid + k*NT.  Every global load is issued
+// before the first LDS write, from an address clamped to row 0 for rows past N (row 0 exists
+// whenever a tile does): the loop it replaces stored each entry right after its own (skippable)
+// load and so waited one global round trip per entry, ~14 in a row per 256-row tile.
+template <int ENTRIES, int NT>
+__device__ __forceinline__ uint32_t load_tile_nbr(const int32_t* __restrict__ nbr,
+                                                  const int32_t* sRow, int32_t* sNbr, int tid) {
+  constexpr int PER = (ENTRIES + NT - 1) / NT;
+  int32_t sv[PER];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int j = min(tid + k * NT, ENTRIES - 1);
+    const int r = j / kTaps, v = j - r * kTaps;
+    const int32_t row = sRow[r];
+    sv[k] = nbr[(int64_t)(row >= 0 ? row : 0) * kTaps + v];
+  }
+  uint32_t mask = 0u;
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int j = tid + k * NT;
+    if (ENTRIES % NT == 0 || j < ENTRIES) {
+      const int r = j / kTaps, v = j - r * kTaps;
+      const int32_t e = sRow[r] >= 0 ? sv[k] : -1;
+      sNbr[j] = e;
+      if (e >= 0) mask |= 1u << v;
+    }
+  }
+  return mask;
+}
+
 // Longest-first tile schedule.  A row tile's running time is about proportional to the taps it
 // uses (the OR of its rows' neighbor masks); with a few rounds of tiles per CU, dealing them in
 // row order leaves CUs idle at the end of the launch.  tile_cost_kernel counts each tile's taps;
@@ -336,14 +367,7 @@ __global__ void __launch_bounds__(64 * WM * WN)
     sRow[r] = (pos < N) ? (order ? order[pos] : (int32_t)pos) : -1;
   }
   __syncthreads();
-  uint32_t mymask = 0u;
-  for (int j = tid; j < BM * kTaps; j += C::NT) {
-    const int r = j / kTaps, v = j - r * kTaps;
-    const int32_t row = sRow[r];
-    const int32_t s = (row >= 0) ? nbr[(int64_t)row * kTaps + v] : -1;
-    sNbr[j] = s;
-    if (s >= 0) mymask |= 1u << v;
-  }
+  uint32_t mymask = load_tile_nbr<BM * kTaps, C::NT>(nbr, sRow, sNbr, tid);
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) mymask |= __shfl_xor(mymask, off, 64);
   if (lane == 0 && mymask) atomicOr(&sMask, mymask);
@@ -647,14 +671,7 @@ __global__ void __launch_bounds__(64 * WM * WN)
     sRow[r] = (pos < N) ? (order ? order[pos] : (int32_t)pos) : -1;
   }
   __syncthreads();
-  uint32_t mymask = 0u;
-  for (int j = tid; j < BM * kTaps; j += C::NT) {
-    int r = j / kTaps, v = j - r * kTaps;
-    int32_t row = sRow[r];
-    int32_t s = (row >= 0) ? nbr[(int64_t)row * kTaps + v] : -1;
-    sNbr[j] = s;
-    if (s >= 0) mymask |= 1u << v;
-  }
+  uint32_t mymask = load_tile_nbr<BM * kTaps, C::NT>(nbr, sRow, sNbr, tid);
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) mymask |= __shfl_xor(mymask, off, 64);
   if (lane == 0 && mymask) atomicOr(&sMask, mymask);
@@ -1215,14 +1232,7 @@ __global__ void __launch_bounds__(kGenThreads)
     sRow[r] = (pos < N) ? (order ? order[pos] : (int32_t)pos) : -1;
   }
   __syncthreads();
-  uint32_t mymask = 0u;
-  for (int j = tid; j < BM * kTaps; j += NT) {
-    const int r = j / kTaps, v = j - r * kTaps;
-    const int32_t row = sRow[r];
-    const int32_t s = (row >= 0) ? nbr[(int64_t)row * kTaps + v] : -1;
-    sNbr[j] = s;
-    if (s >= 0) mymask |= 1u << v;
-  }
+  uint32_t mymask = load_tile_nbr<BM * kTaps, NT>(nbr, sRow, sNbr, tid);
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) mymask |= __shfl_xor(mymask, off, 64);
   if (lane == 0 && mymask) atomicOr(&sMask, mymask);
