@@ -84,6 +84,7 @@ __global__ void __launch_bounds__(64 * kPlanWaves)
   __shared__ uint32_t pbits[kPlanWaves][kOrderWords];
   __shared__ int32_t ppre[kPlanWaves][kOrderWords];
   __shared__ uint32_t hgrp[kPlanWaves][kHash / 16];  // 2 bits per hash entry: halves using it
+  __shared__ int32_t hdum[kPlanWaves][64];            // per-lane target of absent taps' atomics
   __shared__ uint4 table[kPlanWaves][kTableQ];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int64_t t = (int64_t)blockIdx.x * kPlanWaves + w;
@@ -96,6 +97,7 @@ __global__ void __launch_bounds__(64 * kPlanWaves)
   }
   for (int i = lane; i < kOrderWords; i += 64) pbits[w][i] = 0u;
   if (lane < kHash / 16) hgrp[w][lane] = 0u;
+  hdum[w][lane] = -2;
   for (int i = lane; i < kTableQ; i += 64) table[w][i] = make_uint4(0, 0, 0, 0);
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   __builtin_amdgcn_wave_barrier();
@@ -115,59 +117,74 @@ __global__ void __launch_bounds__(64 * kPlanWaves)
   for (int v = 0; v < kTaps; ++v) ev[v] = nr[v];
 #pragma unroll
   for (int v = 0; v < kTaps; ++v) ev[v] = row >= 0 ? ev[v] : -1;
+  // Hash inserts: every present tap's CAS at its home slot is issued before the first result is
+  // used (absent taps aim at the lane's own dummy word, which never holds -1), then the few that
+  // met another key probe on one by one; the priorities likewise go out in one batch.
   int hpos[kTaps];
   uint32_t present = 0;
   bool full = false;
+  int32_t old[kTaps];
 #pragma unroll
   for (int v = 0; v < kTaps; ++v) {
-    const int32_t e = ev[v];
-    hpos[v] = -1;
-    if (e >= 0) {
-      present |= 1u << v;
-      const int prio = v == 13 ? lane : 64 + 64 * v + lane;
-      int h = (int)(((uint32_t)e * 2654435761u) >> kHashShift);
+    hpos[v] = (int)(((uint32_t)ev[v] * 2654435761u) >> kHashShift);
+    if (ev[v] >= 0) present |= 1u << v;
+  }
+#pragma unroll
+  for (int v = 0; v < kTaps; ++v)
+    old[v] = atomicCAS(ev[v] >= 0 ? &hk[hpos[v]] : &hdum[w][lane], -1, ev[v]);
+#pragma unroll
+  for (int v = 0; v < kTaps; ++v) {
+    if (ev[v] >= 0 && old[v] != -1 && old[v] != ev[v]) {
+      int h = hpos[v];
       bool ok = false;
-      for (int probe = 0; probe < kHash; ++probe) {
-        const int32_t old = atomicCAS(&hk[h], -1, e);
-        if (old == -1 || old == e) {
+      for (int probe = 1; probe < kHash; ++probe) {
+        h = (h + 1) & (kHash - 1);
+        const int32_t o = atomicCAS(&hk[h], -1, ev[v]);
+        if (o == -1 || o == ev[v]) {
           ok = true;
           break;
         }
-        h = (h + 1) & (kHash - 1);
       }
-      if (ok) {
-        atomicMin(&hv[h], prio);
-        atomicOr(&hgrp[w][h >> 4], (lane < 32 ? 1u : 2u) << (2 * (h & 15)));
-        hpos[v] = h;
-      } else {
-        full = true;
-      }
+      hpos[v] = ok ? h : -1;
+      full = full || !ok;
     }
+    if (ev[v] < 0) hpos[v] = -1;
   }
+#pragma unroll
+  for (int v = 0; v < kTaps; ++v)
+    atomicMin(hpos[v] >= 0 ? &hv[hpos[v]] : &hdum[w][lane], v == 13 ? lane : 64 + 64 * v + lane);
   const bool overflow = __ballot(full) != 0;
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-  // Distinct count, and per half the rows it uses (split decision).
-  int cnt = 0, ca = 0, cb = 0;
+  // Distinct count; for a tile over the staging also the rows each half uses (split decision).
+  int cnt = 0;
   for (int i = lane; i < kHash / 4; i += 64) {
     const int4 k4 = ((const int4*)hk)[i];
-    const int kk[4] = {k4.x, k4.y, k4.z, k4.w};
+    cnt += (k4.x >= 0) + (k4.y >= 0) + (k4.z >= 0) + (k4.w >= 0);
+  }
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-      if (kk[u] >= 0) {
-        const int h = 4 * i + u;
-        const uint32_t g = (hgrp[w][h >> 4] >> (2 * (h & 15))) & 3u;
-        ++cnt;
+  for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off, 64);
+  int ca = 0, cb = 0;
+  if (cnt >= kPlanStage && cnt <= kPlanSlots - 1 && !overflow) {  // wave-uniform
+#pragma unroll
+    for (int v = 0; v < kTaps; ++v)
+      if (hpos[v] >= 0) atomicOr(&hgrp[w][hpos[v] >> 4], (lane < 32 ? 1u : 2u) << (2 * (hpos[v] & 15)));
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    for (int i = lane; i < kHash; i += 64) {
+      if (hk[i] >= 0) {
+        const uint32_t g = (hgrp[w][i >> 4] >> (2 * (i & 15))) & 3u;
         ca += g & 1u;
         cb += g >> 1;
       }
-  }
+    }
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    cnt += __shfl_xor(cnt, off, 64);
-    ca += __shfl_xor(ca, off, 64);
-    cb += __shfl_xor(cb, off, 64);
+    for (int off = 32; off > 0; off >>= 1) {
+      ca += __shfl_xor(ca, off, 64);
+      cb += __shfl_xor(cb, off, 64);
+    }
   }
   // Per-16-row tap masks.
   uint32_t m = present;
