@@ -253,6 +253,23 @@ def test_planned_two_voxel_shell_split_tiles(pkg, dev, co):
     assert (count >= SPLIT).sum() > 10
 
 
+@pytest.mark.parametrize("co", [32, 64])
+def test_planned_residual_in_place(pkg, dev, co):
+    """The planned kernel's epilogue exchanges columns between lanes before its row stores, so an
+    output that aliases the residual is read and written by different lanes: in place (out is the
+    residual) must give the bits of the separate output, split tiles included."""
+    spec = pkg.workloads.ShellSpec(128, 50.0, 62.0, 2, 0.35, (10, 8))
+    coords = pkg.workloads.shell_coords(spec, 23, 1)
+    print(f"  planned conv in place N={len(coords)} 32->{co}", flush=True)
+    m, f, w, b, res, planned, _ = _pair(pkg, dev, coords, 1, (128, 128, 128), 32, co,
+                                        torch.bfloat16, "residual", seed=5 + co)
+    r2 = res.clone()
+    out = pkg.sparse_conv3d(f, w, b, m, epilogue="residual", residual=r2, out=r2)
+    torch.cuda.synchronize()
+    assert out.data_ptr() == r2.data_ptr()
+    assert torch.equal(r2, planned)
+
+
 def test_plan_two_voxel_shell_layout(pkg, dev):
     """The plan of a small 2-voxel shell against its definition, split tiles included."""
     spec = pkg.workloads.ShellSpec(64, 24.0, 30.0, 2, 0.35, (10, 8))
