@@ -435,16 +435,20 @@ __global__ void __launch_bounds__(kGrThreads)
 #pragma unroll
   for (int j = 0; j < kGrPerThread; ++j)
     if (j < ne) emask[ebeg + j] = gr_mask(my[j]);
-  // Segment marks of a tile (the run starts are no longer needed): a taking entry marks the
-  // first tile slot it fills with (its source position - that slot + kMarkOff); the slots after
-  // it up to the next mark come from the same run.
+  // Segment marks over the chunk's output slots (the run starts are no longer needed): a taking
+  // entry marks the first slot it fills with (its source position - that slot + kMarkOff); the
+  // slots after it up to the next mark come from the same run.  The marks are resolved once for
+  // the whole chunk after the tile loop (a tile's slot 0 is always marked), so a tile costs its
+  // passes plus one seed reduction; resolving them per tile took two more block barriers per
+  // tile, about a third of the kernel.  The seed reduction's barrier orders this clear before
+  // the first mark.
   int32_t* const mark = head;
-  int32_t* const srcpos = idxa;
   constexpr int kMarkOff = 1 << 16;
+  for (int i = tid; i < nc; i += kGrThreads) mark[i] = 0;
   const int ntile = (nc + kGrTile - 1) / kGrTile;
   for (int t = 0; t < ntile; ++t) {
     const int rows = min(kGrTile, nc - t * kGrTile);
-    if (tid < kGrTile) mark[tid] = 0;
+    const int base = t * kGrTile;
     // seed: the first entry with rows left
     uint32_t fa = ~0u;
 #pragma unroll
@@ -502,7 +506,7 @@ __global__ void __launch_bounds__(kGrThreads)
         if (j < ne && left > 0 && (gr_mask(my[j]) & ~orm) == 0u && o < need) {
           const int take = min(left, need - o);
           const int pos = gr_pos(my[j]);
-          mark[fill + o] = pos - (fill + o) + kMarkOff;
+          mark[base + fill + o] = pos - (base + fill + o) + kMarkOff;
           my[j] = gr_make(gr_mask(my[j]), pos + take, left - take);
           o += left;
         }
@@ -513,19 +517,32 @@ __global__ void __launch_bounds__(kGrThreads)
       if (need == 0) break;
       orm |= best != ~0u ? emask[best & 0x3fffu] : ~0u;
     }
-    __syncthreads();  // marks of every thread
-    // Slot r takes its source from the last mark at or before r (inclusive max scan of the
-    // marked slots over the tile's 256 slots, waves 0..3).
-    {
-      int last = wave_incl_max((tid < kGrTile && mark[tid] != 0) ? tid : -1);
-      if (lane == 63) wmax[wid] = last;
-      __syncthreads();
-      for (int ww = 0; ww < wid && ww < kGrTile / 64; ++ww) last = max(last, wmax[ww]);
-      if (tid < rows) srcpos[t * kGrTile + tid] = tid + mark[last] - kMarkOff;
-      __syncthreads();
+  }
+  __syncthreads();  // marks of every thread
+  // Slot r takes its source from the last mark at or before r: thread t scans its slots
+  // [t*P, t*P + P), the last mark before them is an exclusive max scan over the threads.
+  const int r0 = tid * kGrPerThread;
+  int lastj[kGrPerThread];
+  int last = -1;
+#pragma unroll
+  for (int j = 0; j < kGrPerThread; ++j) {
+    if (r0 + j < nc && mark[r0 + j] != 0) last = r0 + j;
+    lastj[j] = last;
+  }
+  const int incl = wave_incl_max(last);
+  if (lane == 63) wmax[wid] = incl;
+  __syncthreads();
+  int before = __shfl_up(incl, 1, 64);
+  if (lane == 0) before = -1;
+  for (int ww = 0; ww < wid; ++ww) before = max(before, wmax[ww]);
+#pragma unroll
+  for (int j = 0; j < kGrPerThread; ++j) {
+    const int r = r0 + j;
+    if (r < nc) {
+      const int l = lastj[j] >= 0 ? lastj[j] : before;
+      order[c0 + r] = vals[c0 + r + mark[l] - kMarkOff];
     }
   }
-  for (int i = tid; i < nc; i += kGrThreads) order[c0 + i] = vals[c0 + srcpos[i]];
 }
 
 
