@@ -424,12 +424,18 @@ __global__ void __launch_bounds__(64 * kGWaves)
 #pragma unroll
     for (int c = 0; c < kGChunks; ++c) idx[c] = list[min(off + 16 * c + j, kPlanSlots - 1)];
   };
+  // Rows are 64 bytes and N < 2^31 here, so one unsigned compare covers 0 <= r < N; the row is
+  // selected as 32 bits before the 64-bit address (left to itself the compiler selected both
+  // halves of the shifted address: 8 instead of 5 VALU instructions per chunk).
+  const uint32_t n32 = (uint32_t)N;
+  const char* const fpiece = (const char*)feats + 16 * p;
   auto gather = [&](int d) {
 #pragma unroll
     for (int c = 0; c < kGChunks; ++c) {
       const int32_t r = idx[c];
-      const bool ok = 16 * c + j < d && r >= 0 && r < N;
-      const uint4 vv = ((const uint4*)(feats + (int64_t)(ok ? r : 0) * 32))[p];
+      uint32_t rr = (uint32_t)r < n32 && 16 * c + j < d ? (uint32_t)r : 0u;
+      asm("" : "+v"(rr));
+      const uint4 vv = *(const uint4*)(fpiece + (uint64_t)rr * 64u);
       x[4 * c] = vv.x;
       x[4 * c + 1] = vv.y;
       x[4 * c + 2] = vv.z;
