@@ -332,6 +332,10 @@ __global__ void __launch_bounds__(64 * kGWaves)
   const int slot_in_half = halves == 2 ? (local >> 1) : local;
   const int blocks_in_half = (int)(gridDim.x >> 3) / halves;
   const int co0 = 32 * half;
+  // The lane's 16-byte store in an output row: columns co0 + 16*(q & 1) + 8*(q >> 1) .. +7
+  // (the epilogue's column exchange), rows reached by one 32 x 32 -> 64-bit multiply-add.
+  const uint32_t row_bytes = (uint32_t)co_total * (uint32_t)sizeof(T);
+  T* const out_lane = out + co0 + 16 * (q & 1) + 8 * (q >> 1);
   if (tid == 0) sTaken = 0;
 
   // Weights (Co,27,32) of this column half: row co, piece p -> [(v*32 + co)*4 + (p ^ ((co>>1)&3))].
@@ -459,7 +463,15 @@ __global__ void __launch_bounds__(64 * kGWaves)
   gather(uc.g);
   uint4 ta, tb2;
   load_tbl(cur, ta, tb2);
-  int32_t row_n = prow[(int64_t)cur * kPlanRows + lane];
+  // Rows of the four 16-row blocks as the epilogue needs them (row 16*rb + l16 in lane (l16, q)),
+  // loaded with the tile's other prefetches rather than broadcast through LDS afterwards.
+  auto load_rows = [&](int t, int32_t (&r4)[4]) {
+    const int32_t* pr = prow + (int64_t)t * kPlanRows + l16;
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) r4[rb] = pr[16 * rb];
+  };
+  int32_t rows_n[4];
+  load_rows(cur, rows_n);
   int32_t pend = take_async();
   int next;
   bool next_second = uc.first;
@@ -495,14 +507,16 @@ __global__ void __launch_bounds__(64 * kGWaves)
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     const Unit u = uc;
     const bool staged = u.g >= 0;
-    int32_t row_c = row_n < N ? row_n : -1;
+    int32_t rows[4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) rows[rb] = rows_n[rb] < N ? rows_n[rb] : -1;
     // Unit `next` (or `cur` again at the end): rows, table and row list go out now; the unit
     // after it gets its metadata and indices.
     const bool has_next = next < t_end;
     uc = decode(meta_n, next_second);
     gather(uc.g);
     load_tbl(nx, ta, tb2);
-    row_n = prow[(int64_t)nx * kPlanRows + lane];
+    load_rows(nx, rows_n);
     int nn;
     const bool nn_second = uc.first;
     if (nn_second) {
@@ -578,7 +592,7 @@ __global__ void __launch_bounds__(64 * kGWaves)
         rd_a(v, a);
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb) {
-          const int32_t r = __shfl(row_c, rb * 16 + l16, 64);
+          const int32_t r = rows[rb];
           const int32_t e = r >= 0 ? nbr[(int64_t)r * kTaps + v] : -1;
           const bool ok = e >= 0 && e < N;
           const uint4 bv4 = ((const uint4*)(feats + (int64_t)(ok ? e : 0) * 32))[q];
@@ -596,9 +610,6 @@ __global__ void __launch_bounds__(64 * kGWaves)
       T v[4];
     };
     if (!u.first) {
-    int32_t rows[4];
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb) rows[rb] = __shfl(row_c, rb * 16 + l16, 64);
     V4 rt[4][2];
     if (EPI == TSC_EPI_BIAS_RESIDUAL) {
 #pragma unroll
@@ -635,7 +646,7 @@ __global__ void __launch_bounds__(64 * kGWaves)
       const auto s1 = __builtin_amdgcn_permlane16_swap(pk[0][1], pk[1][1], false, false);
       const int32_t row = rows[rb];
       if (row >= 0)
-        *(uint4*)(out + (int64_t)row * co_total + co0 + 16 * (q & 1) + 8 * (q >> 1)) =
+        *(uint4*)((char*)out_lane + (uint64_t)(uint32_t)row * row_bytes) =
             make_uint4(s0[0], s1[0], s0[1], s1[1]);
     }
     }  // !u.first
