@@ -631,12 +631,12 @@ __global__ void __launch_bounds__(64 * kGWaves)
 #pragma unroll
           for (int i = 0; i < 4; ++i) xv[i] += (float)rt[rb][cb].v[i];
         }
-        V4 y;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) y.v[i] = (T)xv[i];
-        const uint2 yb = __builtin_bit_cast(uint2, y);
-        pk[cb][0] = yb.x;
-        pk[cb][1] = yb.y;
+        // Pairs as 2-vectors: one v_cvt_pk_{f16,bf16}_f32 each (round to nearest even, as the
+        // scalar conversion; built element by element the compiler emitted two converts and an OR).
+        typedef T t2 __attribute__((ext_vector_type(2)));
+        const t2 lo = {(T)xv[0], (T)xv[1]}, hi = {(T)xv[2], (T)xv[3]};
+        pk[cb][0] = __builtin_bit_cast(uint32_t, lo);
+        pk[cb][1] = __builtin_bit_cast(uint32_t, hi);
       }
       // v_permlane16_swap trades the odd 16-lane rows of its first operand (cb 0) with the even
       // rows of its second (cb 1), between lanes of one l16 and so of one output row: afterwards
