@@ -385,7 +385,7 @@ __global__ void __launch_bounds__(64 * kGWaves)
   // wait for every outstanding load before each dependent one (one vmcnt counts all loads in
   // order), which serialised a tile's ~20 index and row loads into one round trip each.
   //   meta  one load: lanes 0-3 the tile's four 16-row tap masks, lane 4 its distinct-row count
-  //   idx   the list entries of slots off + 16c + j (clamped to the tile's kPlanSlots entries)
+  //   idx   the list entries of slots off + 16c + j (unclamped, see load_idx)
   //   rows  row idx[c] piece p for slots below the count, else row 0 (valid, never staged)
   auto load_meta = [&](int t) {
     return lane < 4 ? (int32_t)prbm[t * 4 + lane] : pcount[t];
@@ -423,10 +423,15 @@ __global__ void __launch_bounds__(64 * kGWaves)
   auto chunk_mask = [](int d) {
     return d > 0 ? __builtin_amdgcn_readfirstlane((1u << ((d + 15) >> 4)) - 1u) : 0u;
   };
+  // Entries off + 16c + j at immediate offsets, unclamped: gather() uses only those below the
+  // unit's count (all inside the tile's list); the others may read the next tile's list or, for
+  // the last tile, the slot tables that follow the lists in the plan buffer (off <= 255, so at
+  // most 16 * kGChunks - 1 entries past its end).
+  static_assert((16 * kGChunks - 1) * 4 <= kPlanTableBytes, "reads past the last list stay in the plan");
   auto load_idx = [&](int t, int off) {
-    const int32_t* list = plist + (int64_t)t * kPlanSlots;
+    const int32_t* list = plist + (int64_t)t * kPlanSlots + off + j;
 #pragma unroll
-    for (int c = 0; c < kGChunks; ++c) idx[c] = list[min(off + 16 * c + j, kPlanSlots - 1)];
+    for (int c = 0; c < kGChunks; ++c) idx[c] = list[16 * c];
   };
   // Rows are 64 bytes and N < 2^31 here, so one unsigned compare covers 0 <= r < N; the row is
   // selected as 32 bits before the 64-bit address (left to itself the compiler selected both
